@@ -1,0 +1,178 @@
+// Internal declarations shared by the HIP translation units of libslmturbo_hip.so.
+// gfx950 (CDNA4) only: wave64, DPP row operations, permlane16/32 swaps, dot8/dot2.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <cstdint>
+#include <string>
+
+#include "../../include/slmturbo.h"
+
+namespace slmt {
+
+// ---------------------------------------------------------------------------
+// Host-side error plumbing: a thread-local message returned by slmt_last_error.
+// ---------------------------------------------------------------------------
+void set_error(const std::string& msg);
+void clear_error();
+int fail(int code, const std::string& msg);
+int check_launch(const char* what);
+
+// Device properties cached per device (compute-unit count).
+int device_cu_count();
+
+// ---------------------------------------------------------------------------
+// Device helpers
+// ---------------------------------------------------------------------------
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float h2f(uint16_t h) {
+  return (float)__builtin_bit_cast(_Float16, h);
+}
+__device__ __forceinline__ uint16_t f2h(float f) {  // round to nearest even
+  return __builtin_bit_cast(uint16_t, (_Float16)f);
+}
+
+// DPP controls (GFX9 encoding).
+enum : int {
+  DPP_QUAD_XOR1 = 0xB1,   // quad_perm [1,0,3,2]
+  DPP_QUAD_XOR2 = 0x4E,   // quad_perm [2,3,0,1]
+  DPP_ROW_ROR4 = 0x124,
+  DPP_ROW_ROR8 = 0x128,
+};
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float x) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0u, __builtin_bit_cast(unsigned, x), CTRL, 0xf, 0xf, false));
+}
+
+// Exchange with the partner row (rows 0<->1, 2<->3) and the partner half-wave.
+// Each swap returns both halves of the exchanged pair; combining them with a
+// commutative op folds "self" and "partner" in every lane.  The two results
+// are copied into scalars before any bit-cast: bit-casting a subscript of the
+// returned vector directly reads element 0 twice with this compiler.
+__device__ __forceinline__ void swap16(float x, float& a, float& b) {
+  const unsigned u = __builtin_bit_cast(unsigned, x);
+  auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  const unsigned r0 = r[0];
+  const unsigned r1 = r[1];
+  a = __builtin_bit_cast(float, r0);
+  b = __builtin_bit_cast(float, r1);
+}
+__device__ __forceinline__ void swap32(float x, float& a, float& b) {
+  const unsigned u = __builtin_bit_cast(unsigned, x);
+  auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  const unsigned r0 = r[0];
+  const unsigned r1 = r[1];
+  a = __builtin_bit_cast(float, r0);
+  b = __builtin_bit_cast(float, r1);
+}
+
+// Reductions over the 16 lanes that share (lane & 3): lanes 4p+g, p = 0..15.
+__device__ __forceinline__ float red16_max(float x) {
+  x = fmaxf(x, dpp_f<DPP_ROW_ROR4>(x));
+  x = fmaxf(x, dpp_f<DPP_ROW_ROR8>(x));
+  float a, b;
+  swap16(x, a, b); x = fmaxf(a, b);
+  swap32(x, a, b); x = fmaxf(a, b);
+  return x;
+}
+__device__ __forceinline__ float red16_sum(float x) {
+  x += dpp_f<DPP_ROW_ROR4>(x);
+  x += dpp_f<DPP_ROW_ROR8>(x);
+  float a, b;
+  swap16(x, a, b); x = a + b;
+  swap32(x, a, b); x = a + b;
+  return x;
+}
+
+// Full wave (64-lane) reductions with the hardware's fminf/fmaxf semantics:
+// NaN operands are ignored and -0 orders below +0.
+__device__ __forceinline__ float wave_min(float x) {
+  x = fminf(x, dpp_f<DPP_QUAD_XOR1>(x));
+  x = fminf(x, dpp_f<DPP_QUAD_XOR2>(x));
+  x = fminf(x, dpp_f<DPP_ROW_ROR4>(x));
+  x = fminf(x, dpp_f<DPP_ROW_ROR8>(x));
+  float a, b;
+  swap16(x, a, b); x = fminf(a, b);
+  swap32(x, a, b); x = fminf(a, b);
+  return x;
+}
+__device__ __forceinline__ float wave_max(float x) {
+  x = fmaxf(x, dpp_f<DPP_QUAD_XOR1>(x));
+  x = fmaxf(x, dpp_f<DPP_QUAD_XOR2>(x));
+  x = fmaxf(x, dpp_f<DPP_ROW_ROR4>(x));
+  x = fmaxf(x, dpp_f<DPP_ROW_ROR8>(x));
+  float a, b;
+  swap16(x, a, b); x = fmaxf(a, b);
+  swap32(x, a, b); x = fmaxf(a, b);
+  return x;
+}
+
+// ---------------------------------------------------------------------------
+// Launchers (defined next to their kernels)
+// ---------------------------------------------------------------------------
+int launch_quantize_store(const void* key, int64_t key_stride, const void* value,
+                          int64_t value_stride, void* cache, int64_t num_slots,
+                          const int64_t* slot_mapping, int64_t N, int KV, int D,
+                          hipStream_t stream);
+
+int launch_quantize_per_channel(const void* x, int KV, int S, int D, void* packed,
+                                void* scale, void* zero, hipStream_t stream);
+
+// Attention source layouts.
+enum SrcMode : int { SRC_PAGED = 0, SRC_TOKEN = 1, SRC_CHANNEL = 2 };
+
+struct AttnParams {
+  // queries: element (b, h, d) at q + b*q_seq_stride + h*q_head_stride + d
+  const uint16_t* q;
+  int64_t q_seq_stride, q_head_stride;
+  // paged source
+  const uint8_t* cache;
+  const void* block_tables;
+  int64_t bt_stride;
+  int bt64;
+  int block_size;
+  int block_shift;   // log2(block_size) when a power of two, else -1
+  int cache_kv;      // KV heads in the cache row
+  int64_t num_blocks;
+  // contiguous sources ([KV_t, S, D/2] codes; rulers [KV_t, S] or [KV_t, D])
+  const uint8_t* kp;
+  const uint8_t* vp;
+  const uint16_t* kr0;  // k_min   | k_scale
+  const uint16_t* kr1;  // k_step  | k_zero
+  const uint16_t* vr0;  // v_min   | v_scale
+  const uint16_t* vr1;  // v_step  | v_zero
+  int s_rows;           // S of the contiguous tensors
+  int use_quant;
+  // sequences: L_b = seq_lens[b], or fixed_len, or min(fixed_len, b+1) (causal rows)
+  const int32_t* seq_lens;
+  int fixed_len;
+  int causal_rows;
+  int B, H, G;           // G = H / num_kv_heads
+  int heads_per_group;   // query heads per workgroup (multiple of 4)
+  // output: element (b, h, d) at out + b*out_seq_stride + h*out_head_stride + d
+  void* out;
+  int out_f16;
+  int64_t out_seq_stride, out_head_stride;
+  // workspace
+  float* part_o;    // [W][2][H][D]
+  float* part_ml;   // [W][2][H][2]
+  int* counters;    // [groups][B]
+  int W;            // workgroups per head group (grid.x)
+  int min_tiles;    // minimum 16-token tiles per workgroup
+};
+
+// Geometry chosen on the host for a launch.
+struct AttnPlan {
+  int heads_per_group, groups, waves, W;
+  size_t lds_bytes;
+};
+
+int plan_attention(int B, int H, int G, int D, AttnPlan* plan);
+int64_t attention_workspace_bytes(int B, int H, int KV, int D);
+int launch_attention(int mode, int D, AttnParams& p, void* workspace, int64_t ws_bytes,
+                     hipStream_t stream);
+
+}  // namespace slmt

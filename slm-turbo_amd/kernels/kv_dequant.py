@@ -1,0 +1,426 @@
+# =============================================================================
+#  kernels/kv_dequant.py  (MI355X / gfx950)
+#
+#  Fused 4-bit KV-quantized attention kernels -- HIP, hand-written for CDNA4.
+#
+#  Python API, signature-compatible with the reference's kernels/kv_dequant.py:
+#
+#      kv_dequant_decode_attention(...)                 -> [H, 1, D] fp32
+#      kv_dequant_prefill_attention(...)                -> [H, M, D] fp32
+#      kv_dequant_decode_per_token_attention(...)       -> [H, 1, D] fp32
+#      kv_dequant_decode_per_token_paged_attention(...) -> [H, 1, D] fp32
+#      kv_quantize_store(...)                           -> None (writes cache)
+#
+#  plus the batched paged decode the vLLM backend uses (one launch per layer
+#  for the whole batch) and the per-channel quantizer on the GPU:
+#
+#      kv_dequant_decode_paged_batched(...)             -> [B, H, D]
+#      quantize_per_channel(x) / quantize_kv(k, v)
+#
+#  The device code is libslmturbo_hip.so (slm-turbo_amd/csrc), reached through
+#  its C ABI (include/slmturbo.h) with ctypes; launches go to the current torch
+#  stream.  There is no CPU path: like the reference, calls raise when the
+#  native library or a GPU is unavailable.
+# =============================================================================
+from __future__ import annotations
+
+import math
+import threading
+
+import torch
+
+from . import _native
+
+__all__ = [
+    "kv_dequant_decode_attention",
+    "kv_dequant_prefill_attention",
+    "kv_dequant_decode_per_token_attention",
+    "kv_quantize_store",
+    "kv_dequant_decode_per_token_paged_attention",
+    "kv_dequant_decode_paged_batched",
+    "quantize_per_channel",
+    "quantize_kv",
+]
+
+_SUPPORTED_D = (64, 80, 128)
+
+
+def _load_native_extension():
+    """Load (once) the HIP library; a failure is cached and re-raised
+    (reference kernels/kv_dequant.py:47-86)."""
+    return _native.load()
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _ptr(t: torch.Tensor) -> int:
+    return t.data_ptr()
+
+
+# Workspace per (device, stream): zero-filled once; the kernels leave their
+# arrival counters at zero, so calls ordered on one stream can share it.
+_ws_lock = threading.Lock()
+_ws_cache: dict = {}
+
+
+def _workspace(lib, device: torch.device, B: int, H: int, KV: int, D: int) -> tuple[int, int]:
+    need = int(lib.slmt_attention_workspace_bytes(B, H, KV, D))
+    if need < 0:
+        raise RuntimeError(_native.last_error(lib))
+    key = (device.index, _stream(device))
+    with _ws_lock:
+        buf = _ws_cache.get(key)
+        if buf is None or buf.numel() < need:
+            buf = torch.zeros(max(need, 1 << 20), dtype=torch.uint8, device=device)
+            _ws_cache[key] = buf
+    return buf.data_ptr(), buf.numel()
+
+
+def _require(cond: bool, msg: str) -> None:
+    if not cond:
+        raise RuntimeError(msg)
+
+
+def _check_common(q, k_packed, k_scale, k_zero, v_packed, v_scale, v_zero, phase, num_kv_heads):
+    """Native-side validation (reference kernels/kv_dequant_cuda.cu:53-76)."""
+    _require(q.is_cuda, f"{phase}: q must be a CUDA tensor")
+    _require(q.dtype == torch.float16, f"{phase}: q must be fp16")
+    _require(k_packed.is_cuda and v_packed.is_cuda, f"{phase}: packed KV must be CUDA tensors")
+    _require(k_packed.dtype == torch.uint8 and v_packed.dtype == torch.uint8, f"{phase}: packed KV must be uint8")
+    for t in (k_scale, k_zero, v_scale, v_zero):
+        _require(t.is_cuda and t.dtype == torch.float16, f"{phase}: scale/zero tensors must be fp16 CUDA")
+    D, D2 = q.size(2), k_packed.size(2)
+    _require(D == 2 * D2, f"{phase}: D ({D}) must be 2 * D2 ({D2})")
+    H = q.size(0)
+    _require(num_kv_heads > 0 and H % num_kv_heads == 0,
+             f"{phase}: num_kv_heads {num_kv_heads} must divide query heads {H}")
+
+
+# =============================================================================
+#  DECODE attention (per-channel)
+# =============================================================================
+def kv_dequant_decode_attention(
+    q, k_packed, k_scale, k_zero, v_packed, v_scale, v_zero,
+    BLOCK_N=64, use_quant=True, num_kv_heads=None,
+):
+    """Fused 4-bit per-channel decode.  Returns [H, 1, D] fp32.
+
+    Same arguments and checks as the reference (kernels/kv_dequant.py:92-123):
+        q [H, 1, D] fp16; k/v_packed [KV, S, D//2] uint8; k/v_scale, k/v_zero
+        [KV, D] fp16; BLOCK_N in (32, 64); use_quant False attends over raw
+        nibbles; num_kv_heads defaults to k_packed.shape[0].
+    """
+    H, _, D = q.shape
+    KV, S, D2 = k_packed.shape
+    assert D == D2 * 2, f"D {D} != 2*D2 {D2}"
+    assert D in (64, 80, 128), f"head_dim must be 64/80/128, got {D}"
+    assert BLOCK_N in (32, 64), f"BLOCK_N must be 32 or 64, got {BLOCK_N}"
+    num_kv_heads = KV if num_kv_heads is None else num_kv_heads
+    assert H % num_kv_heads == 0, f"H {H} not divisible by num_kv_heads {num_kv_heads}"
+    assert q.shape == (H, 1, D), f"q {q.shape} != {(H, 1, D)}"
+
+    lib = _load_native_extension()
+    phase = "kv_dequant_decode"
+    _check_common(q, k_packed, k_scale, k_zero, v_packed, v_scale, v_zero, phase, num_kv_heads)
+    _require(num_kv_heads <= KV, f"{phase}: num_kv_heads {num_kv_heads} exceeds the packed KV heads {KV}")
+    dev = q.device
+    with torch.cuda.device(dev):
+        out = torch.empty((H, 1, D), dtype=torch.float32, device=dev)
+        if S == 0:  # the reference divides 0 by 0
+            return out.fill_(math.nan)
+        q, k_packed, k_scale, k_zero, v_packed, v_scale, v_zero = (
+            t.contiguous() for t in (q, k_packed, k_scale, k_zero, v_packed, v_scale, v_zero))
+        ws, ws_bytes = _workspace(lib, dev, 1, H, num_kv_heads, D)
+        rc = lib.slmt_decode_per_channel(
+            _ptr(q), _ptr(k_packed), _ptr(k_scale), _ptr(k_zero), _ptr(v_packed), _ptr(v_scale),
+            _ptr(v_zero), H, KV, num_kv_heads, S, D, BLOCK_N, int(bool(use_quant)), _ptr(out),
+            ws, ws_bytes, _stream(dev))
+        _native.check(lib, rc)
+    return out
+
+
+# =============================================================================
+#  PREFILL attention (per-channel)
+# =============================================================================
+def kv_dequant_prefill_attention(
+    q, k_packed, k_scale, k_zero, v_packed, v_scale, v_zero,
+    BLOCK_M=None, BLOCK_N=None, causal=True, use_quant=True, num_kv_heads=None,
+):
+    """Fused 4-bit per-channel prefill.  Returns [H, M, D] fp32.
+
+    Same arguments, defaults and tile checks as the reference
+    (kernels/kv_dequant.py:129-177).  BLOCK_M/BLOCK_N are validated for API
+    compatibility; they do not change the result.  With causal=True query m
+    sees keys n <= m (both indexed from 0).
+    """
+    H, M, D = q.shape
+    KV, S, D2 = k_packed.shape
+    assert D == D2 * 2, f"D {D} != 2*D2 {D2}"
+    assert D in (64, 80, 128), f"head_dim must be 64/80/128, got {D}"
+    assert q.device == k_packed.device
+    num_kv_heads = KV if num_kv_heads is None else num_kv_heads
+    assert H % num_kv_heads == 0, f"H {H} not divisible by num_kv_heads {num_kv_heads}"
+    if BLOCK_M is None:
+        BLOCK_M = 16
+    if BLOCK_N is None:
+        BLOCK_N = 64 if D == 64 else 32
+    assert BLOCK_M in (16, 32), f"BLOCK_M must be 16 or 32, got {BLOCK_M}"
+    assert BLOCK_N in (32, 64), f"BLOCK_N must be 32 or 64, got {BLOCK_N}"
+    if D != 64:
+        assert (BLOCK_M, BLOCK_N) == (16, 32), (
+            f"head_dim {D}: only (BLOCK_M=16, BLOCK_N=32) fits the "
+            f"48 KB shared budget; got ({BLOCK_M}, {BLOCK_N})"
+        )
+
+    lib = _load_native_extension()
+    phase = "kv_dequant_prefill"
+    _check_common(q, k_packed, k_scale, k_zero, v_packed, v_scale, v_zero, phase, num_kv_heads)
+    _require(q.dim() == 3, f"{phase}: q must be [H, M, D], got {list(q.shape)}")
+    _require(num_kv_heads <= KV, f"{phase}: num_kv_heads {num_kv_heads} exceeds the packed KV heads {KV}")
+    dev = q.device
+    with torch.cuda.device(dev):
+        out = torch.empty((H, M, D), dtype=torch.float32, device=dev)
+        if M == 0:
+            return out
+        if S == 0:
+            return out.fill_(math.nan)
+        q, k_packed, k_scale, k_zero, v_packed, v_scale, v_zero = (
+            t.contiguous() for t in (q, k_packed, k_scale, k_zero, v_packed, v_scale, v_zero))
+        ws, ws_bytes = _workspace(lib, dev, M, H, num_kv_heads, D)
+        rc = lib.slmt_prefill_per_channel(
+            _ptr(q), _ptr(k_packed), _ptr(k_scale), _ptr(k_zero), _ptr(v_packed), _ptr(v_scale),
+            _ptr(v_zero), H, KV, num_kv_heads, M, S, D, BLOCK_M, BLOCK_N, int(bool(causal)),
+            int(bool(use_quant)), _ptr(out), ws, ws_bytes, _stream(dev))
+        _native.check(lib, rc)
+    return out
+
+
+# =============================================================================
+#  PER-TOKEN DECODE attention  (contiguous per-token buffers)
+# =============================================================================
+def kv_dequant_decode_per_token_attention(
+    q, k_packed, k_min, k_step, v_packed, v_min, v_step,
+    BLOCK_N=64, num_kv_heads=None,
+):
+    """Per-token (min, step) decode over contiguous buffers.  Returns [H, 1, D]
+    fp32 (reference kernels/kv_dequant.py:189-217).
+
+        q [H, 1, D] fp16; k/v_packed [KV, S, D//2] uint8;
+        k/v_min, k/v_step [KV, S] fp16; value = nibble * step + min.
+    """
+    H, _, D = q.shape
+    KV, S, D2 = k_packed.shape
+    assert D == D2 * 2, f"D {D} != 2*D2 {D2}"
+    assert D in (64, 80, 128), f"head_dim must be 64/80/128, got {D}"
+    assert BLOCK_N in (32, 64), f"BLOCK_N must be 32 or 64, got {BLOCK_N}"
+    num_kv_heads = KV if num_kv_heads is None else num_kv_heads
+    assert H % num_kv_heads == 0, f"H {H} not divisible by num_kv_heads {num_kv_heads}"
+
+    lib = _load_native_extension()
+    phase = "per-token decode"
+    _require(q.is_cuda and q.dtype == torch.float16, f"{phase}: q must be fp16 CUDA")
+    _require(q.dim() == 3 and q.size(1) == 1, f"{phase}: q must be [H, 1, D], got {list(q.shape)}")
+    _require(k_packed.is_cuda and v_packed.is_cuda and k_packed.dtype == torch.uint8
+             and v_packed.dtype == torch.uint8, f"{phase}: packed KV must be uint8 CUDA tensors")
+    for t in (k_min, k_step, v_min, v_step):
+        _require(t.is_cuda and t.dtype == torch.float16 and tuple(t.shape) == (KV, S),
+                 f"{phase}: min/step tensors must be fp16 CUDA [KV, S]")
+    _require(num_kv_heads <= KV, f"{phase}: num_kv_heads {num_kv_heads} exceeds the packed KV heads {KV}")
+    dev = q.device
+    with torch.cuda.device(dev):
+        out = torch.empty((H, 1, D), dtype=torch.float32, device=dev)
+        if S == 0:
+            return out.fill_(math.nan)
+        q, k_packed, k_min, k_step, v_packed, v_min, v_step = (
+            t.contiguous() for t in (q, k_packed, k_min, k_step, v_packed, v_min, v_step))
+        ws, ws_bytes = _workspace(lib, dev, 1, H, num_kv_heads, D)
+        rc = lib.slmt_decode_per_token(
+            _ptr(q), _ptr(k_packed), _ptr(k_min), _ptr(k_step), _ptr(v_packed), _ptr(v_min),
+            _ptr(v_step), H, KV, num_kv_heads, S, D, BLOCK_N, _ptr(out), ws, ws_bytes, _stream(dev))
+        _native.check(lib, rc)
+    return out
+
+
+# =============================================================================
+#  QUANTIZE-ON-WRITE store into the packed paged cache
+# =============================================================================
+def kv_quantize_store(key, value, kv_cache, slot_mapping, block_size):
+    """Quantize-on-write: pack fp16 K/V rows into the 4-bit cache slots
+    (reference kernels/kv_dequant.py:220-233).
+
+        key, value:   [N, KV, D] fp16 (rows may be strided over tokens)
+        kv_cache:     [num_blocks, block_size, KV, D+8] uint8, contiguous
+        slot_mapping: [N] int64; slot < 0 is skipped
+        block_size:   the cache's block size
+    """
+    assert key.dim() == 3, f"key must be [N, KV, D], got {key.shape}"
+    assert kv_cache.is_contiguous(), "kv_cache must be contiguous"
+    lib = _load_native_extension()
+    _require(key.is_cuda and key.dtype == torch.float16 and value.is_cuda and value.dtype == torch.float16,
+             "store: key/value must be fp16 CUDA")
+    _require(kv_cache.dtype == torch.uint8, "store: kv_cache must be uint8")
+    N, KV, D = key.shape
+    _require(D in _SUPPORTED_D, f"store: head_dim must be 64/80/128, got {D}")
+    SLOT = D + 8
+    _require(kv_cache.size(-1) == SLOT, f"store: cache slot size {kv_cache.size(-1)} != expected {SLOT}")
+    _require(slot_mapping.dtype == torch.int64 and slot_mapping.numel() == N,
+             "store: slot_mapping must be int64 of length N")
+    _require(tuple(value.shape) == (N, KV, D), f"store: value must be [N, KV, D] like key, got {list(value.shape)}")
+    _require(kv_cache.dim() == 4 and kv_cache.size(2) == KV and kv_cache.size(1) == block_size,
+             f"store: kv_cache must be [num_blocks, {block_size}, {KV}, {SLOT}], got {list(kv_cache.shape)}")
+    dev = key.device
+    with torch.cuda.device(dev):
+        # token-strided rows are read in place; anything else is made contiguous
+        def rows(t):
+            if t.stride(2) == 1 and t.stride(1) == D and t.stride(0) % 2 == 0:
+                return t, t.stride(0)
+            t = t.contiguous()
+            return t, KV * D
+        key, ks = rows(key)
+        value, vs = rows(value)
+        slot_mapping = slot_mapping.contiguous()
+        rc = lib.slmt_quantize_store(
+            _ptr(key), ks, _ptr(value), vs, _ptr(kv_cache), kv_cache.size(0), int(block_size),
+            _ptr(slot_mapping), N, KV, D, _stream(dev))
+        _native.check(lib, rc)
+
+
+# =============================================================================
+#  PAGED PER-TOKEN DECODE (one request, reference API)
+# =============================================================================
+def kv_dequant_decode_per_token_paged_attention(
+    q, kv_cache, block_table, seq_len, block_size, num_kv_heads,
+):
+    """Paged per-token decode for one request, reading the packed cache through
+    its block table.  Returns [H, 1, D] fp32
+    (reference kernels/kv_dequant.py:236-257).
+
+        q [H, 1, D] fp16; kv_cache [num_blocks, block_size, KV, D+8] uint8;
+        block_table [max_blocks] int64 (int32 accepted); seq_len, block_size,
+        num_kv_heads ints.
+    """
+    H, _, D = q.shape
+    assert D in (64, 80, 128), f"head_dim must be 64/80/128, got {D}"
+    assert H % num_kv_heads == 0, f"H {H} not divisible by num_kv_heads {num_kv_heads}"
+    assert kv_cache.size(-1) == D + 8, f"cache slot must be D+8, got {kv_cache.size(-1)}"
+    lib = _load_native_extension()
+    _require(q.is_cuda and q.dtype == torch.float16, "paged decode: q must be fp16 CUDA")
+    _require(q.dim() == 3 and q.size(1) == 1, f"paged decode: q must be [H, 1, D], got {list(q.shape)}")
+    _require(kv_cache.dtype == torch.uint8, "paged decode: kv_cache must be uint8")
+    _require(kv_cache.size(-1) == D + 8, "paged decode: cache slot size must be D+8")
+    _require(kv_cache.dim() == 4 and kv_cache.size(2) == num_kv_heads,
+             f"paged decode: kv_cache must be [num_blocks, block_size, {num_kv_heads}, {D + 8}]")
+    _require(block_table.dtype in (torch.int64, torch.int32), "paged decode: block_table must be int64 or int32")
+    seq_len = int(seq_len)
+    dev = q.device
+    with torch.cuda.device(dev):
+        out = torch.empty((H, 1, D), dtype=torch.float32, device=dev)
+        if seq_len <= 0:
+            return out.fill_(math.nan)
+        _require(block_table.numel() * int(block_size) >= seq_len,
+                 f"paged decode: block_table holds {block_table.numel()} blocks, fewer than seq_len {seq_len} needs")
+        q = q.contiguous()
+        kv_cache = kv_cache.contiguous()
+        block_table = block_table.contiguous()
+        ws, ws_bytes = _workspace(lib, dev, 1, H, num_kv_heads, D)
+        rc = lib.slmt_decode_paged(
+            _ptr(q), H * D, D, _ptr(kv_cache), kv_cache.size(0), int(block_size), _ptr(block_table),
+            64 if block_table.dtype == torch.int64 else 32, 0, None, seq_len, 1, H, num_kv_heads, D,
+            _ptr(out), _native.OUT_F32, H * D, D, ws, ws_bytes, _stream(dev))
+        _native.check(lib, rc)
+    return out
+
+
+# =============================================================================
+#  BATCHED PAGED DECODE (one launch for a whole decode batch)
+# =============================================================================
+def kv_dequant_decode_paged_batched(
+    q, kv_cache, block_tables, seq_lens, block_size, num_kv_heads, out=None, out_dtype=None,
+):
+    """Paged per-token decode for a batch in ONE launch.  Returns [B, H, D].
+
+    The batched form of ``kv_dequant_decode_per_token_paged_attention`` that the
+    vLLM backend calls once per layer instead of once per request
+    (reference adapters/vllm_adapter.py:271-279):
+        q            [B, H, D] fp16 (strides: any, with unit stride over D)
+        kv_cache     [num_blocks, block_size, KV, D+8] uint8
+        block_tables [B, max_blocks] int32 or int64 (device)
+        seq_lens     [B] int32 (device; read by the kernel, no host sync)
+        out          optional [B, H, D] fp32/fp16 tensor written in place
+        out_dtype    fp32 (default) or fp16 when ``out`` is not given
+    Sequences of length 0 produce zeros.
+    """
+    assert q.dim() == 3, f"q must be [B, H, D], got {tuple(q.shape)}"
+    B, H, D = q.shape
+    assert D in (64, 80, 128), f"head_dim must be 64/80/128, got {D}"
+    assert H % num_kv_heads == 0, f"H {H} not divisible by num_kv_heads {num_kv_heads}"
+    assert kv_cache.size(-1) == D + 8, f"cache slot must be D+8, got {kv_cache.size(-1)}"
+    lib = _load_native_extension()
+    _require(q.is_cuda and q.dtype == torch.float16, "paged decode: q must be fp16 CUDA")
+    _require(kv_cache.is_cuda and kv_cache.dtype == torch.uint8 and kv_cache.is_contiguous(),
+             "paged decode: kv_cache must be a contiguous uint8 CUDA tensor")
+    _require(kv_cache.dim() == 4 and kv_cache.size(1) == block_size and kv_cache.size(2) == num_kv_heads,
+             f"paged decode: kv_cache must be [num_blocks, {block_size}, {num_kv_heads}, {D + 8}]")
+    _require(block_tables.dim() == 2 and block_tables.size(0) == B and block_tables.stride(1) == 1
+             and block_tables.dtype in (torch.int32, torch.int64) and block_tables.is_cuda,
+             "paged decode: block_tables must be an int32/int64 CUDA tensor [B, max_blocks]")
+    _require(seq_lens.is_cuda and seq_lens.dtype == torch.int32 and seq_lens.numel() == B,
+             "paged decode: seq_lens must be an int32 CUDA tensor [B]")
+    dev = q.device
+    with torch.cuda.device(dev):
+        if out is None:
+            out = torch.empty((B, H, D), dtype=out_dtype or torch.float32, device=dev)
+        _require(out.dtype in (torch.float32, torch.float16) and tuple(out.shape) == (B, H, D)
+                 and out.stride(2) == 1, "paged decode: out must be fp32/fp16 [B, H, D] with unit stride over D")
+        if B == 0:
+            return out
+        if q.stride(2) != 1 or q.stride(1) % 8 or q.stride(0) % 8 or q.data_ptr() % 16:
+            q = q.contiguous()
+        seq_lens = seq_lens.contiguous()
+        ws, ws_bytes = _workspace(lib, dev, B, H, num_kv_heads, D)
+        rc = lib.slmt_decode_paged(
+            _ptr(q), q.stride(0), q.stride(1), _ptr(kv_cache), kv_cache.size(0), int(block_size),
+            _ptr(block_tables), 64 if block_tables.dtype == torch.int64 else 32, block_tables.stride(0),
+            _ptr(seq_lens), 0, B, H, num_kv_heads, D, _ptr(out),
+            _native.OUT_F16 if out.dtype == torch.float16 else _native.OUT_F32,
+            out.stride(0), out.stride(1), ws, ws_bytes, _stream(dev))
+        _native.check(lib, rc)
+    return out
+
+
+# =============================================================================
+#  PER-CHANNEL QUANTIZER on the GPU
+# =============================================================================
+def quantize_per_channel(x):
+    """Per-channel asymmetric 4-bit quantizer of the standalone path, on the GPU.
+
+    Bit-exact with the reference's host torch code
+    (kernels/benchmark/benchmark.py:26-56):  x [KV, S, D] fp16 ->
+    (packed [KV, S, D//2] uint8, scale [KV, D] fp16, zero [KV, D] fp16).
+    """
+    assert x.dim() == 3, f"x must be [KV, S, D], got {tuple(x.shape)}"
+    KV, S, D = x.shape
+    assert D in (64, 80, 128), f"head_dim must be 64/80/128, got {D}"
+    lib = _load_native_extension()
+    _require(x.is_cuda and x.dtype == torch.float16, "quantize: x must be fp16 CUDA")
+    _require(S >= 1, "quantize: the sequence axis must not be empty")
+    dev = x.device
+    with torch.cuda.device(dev):
+        x = x.contiguous()
+        packed = torch.empty((KV, S, D // 2), dtype=torch.uint8, device=dev)
+        scale = torch.empty((KV, D), dtype=torch.float16, device=dev)
+        zero = torch.empty((KV, D), dtype=torch.float16, device=dev)
+        rc = lib.slmt_quantize_per_channel(_ptr(x), KV, S, D, _ptr(packed), _ptr(scale), _ptr(zero),
+                                           _stream(dev))
+        _native.check(lib, rc)
+    return packed, scale, zero
+
+
+def quantize_kv(k, v):
+    """(k_packed, k_scale, k_zero, v_packed, v_scale, v_zero), like the
+    reference's quantize_kv (kernels/benchmark/benchmark.py:69-74)."""
+    kp, ks, kz = quantize_per_channel(k)
+    vp, vs, vz = quantize_per_channel(v)
+    return kp, ks, kz, vp, vs, vz

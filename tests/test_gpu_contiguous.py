@@ -1,0 +1,156 @@
+"""GPU parity of the standalone (contiguous) entry points against the oracle:
+per-channel decode and prefill (reference kernels/kv_dequant_kernels.cuh:113-502),
+per-token decode (:528-655) and the per-channel quantizer on the GPU
+(reference host code kernels/benchmark/benchmark.py:26-56, bit-exact)."""
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from common import assert_close, kv_values
+from oracle import attention as oa
+from oracle import quant as oq
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+GOLDEN = Path(__file__).resolve().parent / "golden" / "per_channel_quant.npz"
+
+
+def _kd():
+    from kernels import kv_dequant
+    return kv_dequant
+
+
+def _outliers(x: torch.Tensor, gen, frac=0.01, factor=8.0):
+    KV, S, D = x.shape
+    n = max(1, int(np.ceil(frac * KV * D)))
+    for c in torch.randperm(KV * D, generator=gen)[:n].tolist():
+        x[c // D, :, c % D] *= factor
+    return x
+
+
+# ------------------------------------------------------------------ quantizer
+def _same_fp16(got, ref):
+    """Bit-exact fp16, except that any NaN matches any NaN (the sign and
+    payload of a NaN produced by 0/0 differ between x86 and the GPU)."""
+    same = (got.view(np.uint16) == ref.view(np.uint16)) | (np.isnan(got) & np.isnan(ref))
+    assert same.all(), f"{int((~same).sum())} values differ, first at {np.argwhere(~same)[:3].tolist()}"
+
+
+@pytest.mark.parametrize("name", sorted({k.split("__")[0] for k in np.load(GOLDEN).files}))
+def test_quantize_per_channel_matches_reference_golden(name):
+    z = np.load(GOLDEN)
+    x = torch.from_numpy(z[f"{name}__x"].view(np.float16).copy())
+    packed, scale, zero = _kd().quantize_per_channel(x.to(DEV))
+    torch.cuda.synchronize()
+    _same_fp16(scale.cpu().numpy(), z[f"{name}__scale"].view(np.float16))
+    _same_fp16(zero.cpu().numpy(), z[f"{name}__zero"].view(np.float16))
+    assert np.array_equal(packed.cpu().numpy(), z[f"{name}__packed"])
+
+
+@pytest.mark.parametrize("KV,S,D", [(4, 512, 64), (2, 2048, 128), (2, 333, 80), (8, 1, 128)])
+def test_quantize_per_channel_matches_oracle(KV, S, D):
+    g = torch.Generator().manual_seed(S + D)
+    x = _outliers(torch.randn(KV, S, D, generator=g), g).half()
+    packed, scale, zero = _kd().quantize_per_channel(x.to(DEV))
+    torch.cuda.synchronize()
+    s_ref, z_ref = oq.compute_scale_zero(x.numpy())
+    p_ref = oq.quantize_tensor(x.numpy(), s_ref, z_ref)
+    _same_fp16(scale.cpu().numpy(), s_ref)
+    _same_fp16(zero.cpu().numpy(), z_ref)
+    assert np.array_equal(packed.cpu().numpy(), p_ref)
+
+
+# ------------------------------------------------------------------ per-channel decode
+def _pc_inputs(seed, H, KV, S, D, outliers=False):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(H, 1, D, generator=g).half()
+    k = torch.randn(KV, S, D, generator=g)
+    v = torch.randn(KV, S, D, generator=g)
+    if outliers:
+        k, v = _outliers(k, g), _outliers(v, g)
+    kp, ks, kz, vp, vs, vz = oq.quantize_kv(k.half().numpy(), v.half().numpy())
+    return q, [torch.from_numpy(a) for a in (kp, ks, kz, vp, vs, vz)]
+
+
+@pytest.mark.parametrize("H,KV,D,S,outl", [(4, 4, 64, 512, False),            # config 1
+                                           (12, 2, 128, 512, True),            # config 2
+                                           (12, 2, 128, 1024, True),
+                                           (12, 2, 128, 2048, True),
+                                           (32, 4, 64, 1024, False), (32, 8, 128, 700, False),
+                                           (14, 2, 64, 333, False), (8, 8, 80, 97, False)])
+def test_decode_per_channel(H, KV, D, S, outl):
+    q, t = _pc_inputs(H * 7 + S, H, KV, S, D, outl)
+    out = _kd().kv_dequant_decode_attention(q.to(DEV), *[x.to(DEV) for x in t], num_kv_heads=KV)
+    torch.cuda.synchronize()
+    assert out.shape == (H, 1, D) and out.dtype == torch.float32
+    ref = oa.decode_per_channel(q.numpy(), *[x.numpy() for x in t])
+    assert_close(out.cpu().numpy(), ref, what="per-channel decode")
+    # The reference benchmark's own check rounds the dequantized KV to fp16
+    # before attending (kernels/benchmark/benchmark.py:112).  Against that
+    # oracle the bar widens by the two oracles' own difference.
+    ref16 = oa.decode_per_channel(q.numpy(), *[x.numpy() for x in t], round_fp16=True)
+    gap = np.abs(ref16 - ref).max()
+    assert_close(out.cpu().numpy(), ref16, atol=2e-3 + gap, what="vs fp16-rounded dequant")
+
+
+def test_decode_per_channel_raw_nibbles_and_block_n():
+    q, t = _pc_inputs(5, 8, 2, 300, 128)
+    kd = _kd()
+    raw = kd.kv_dequant_decode_attention(q.to(DEV), *[x.to(DEV) for x in t], BLOCK_N=32,
+                                         use_quant=False, num_kv_heads=2)
+    torch.cuda.synchronize()
+    ref = oa.decode_per_channel(q.numpy(), *[x.numpy() for x in t], use_quant=False)
+    assert_close(raw.cpu().numpy(), ref, what="use_quant=False")
+
+
+def test_decode_per_channel_fewer_kv_heads_than_tensor():
+    """num_kv_heads < k_packed.shape[0]: only the first heads are attended."""
+    q, t = _pc_inputs(6, 8, 4, 200, 64)
+    out = _kd().kv_dequant_decode_attention(q.to(DEV), *[x.to(DEV) for x in t], num_kv_heads=2)
+    torch.cuda.synchronize()
+    kp, ks, kz, vp, vs, vz = [x.numpy() for x in t]
+    ref = oa.decode_per_channel(q.numpy(), kp[:2], ks[:2], kz[:2], vp[:2], vs[:2], vz[:2])
+    assert_close(out.cpu().numpy(), ref)
+
+
+# ------------------------------------------------------------------ prefill
+@pytest.mark.parametrize("H,KV,D,M,S,causal", [(32, 4, 64, 256, 256, True), (14, 2, 64, 100, 100, True),
+                                               (8, 2, 128, 64, 64, True), (8, 8, 80, 50, 50, False),
+                                               (4, 4, 64, 40, 70, True), (4, 2, 64, 70, 40, True)])
+def test_prefill_per_channel(H, KV, D, M, S, causal):
+    g = torch.Generator().manual_seed(M * 3 + S)
+    q = torch.randn(H, M, D, generator=g).half()
+    k = torch.randn(KV, S, D, generator=g).half()
+    v = torch.randn(KV, S, D, generator=g).half()
+    kp, ks, kz, vp, vs, vz = [torch.from_numpy(a) for a in oq.quantize_kv(k.numpy(), v.numpy())]
+    kw = {} if D == 64 else {"BLOCK_M": 16, "BLOCK_N": 32}
+    out = _kd().kv_dequant_prefill_attention(q.to(DEV), kp.to(DEV), ks.to(DEV), kz.to(DEV), vp.to(DEV),
+                                             vs.to(DEV), vz.to(DEV), causal=causal, num_kv_heads=KV, **kw)
+    torch.cuda.synchronize()
+    ref = oa.prefill_per_channel(q.numpy(), kp.numpy(), ks.numpy(), kz.numpy(), vp.numpy(), vs.numpy(),
+                                 vz.numpy(), causal=causal)
+    assert out.shape == (H, M, D)
+    assert_close(out.cpu().numpy(), ref, what="prefill")
+
+
+# ------------------------------------------------------------------ per-token contiguous decode
+@pytest.mark.parametrize("H,KV,D,S", [(32, 8, 128, 1000), (4, 4, 64, 17), (12, 2, 80, 333)])
+def test_decode_per_token_contiguous(H, KV, D, S):
+    g = torch.Generator().manual_seed(S)
+    q = torch.randn(H, 1, D, generator=g).half()
+    k = kv_values(g, (S, KV, D))
+    v = kv_values(g, (S, KV, D))
+    # quantize rows with the oracle store into a scratch cache, then unpack to the contiguous layout
+    cache = np.zeros((S, 1, KV, D + 8), dtype=np.uint8)
+    oq.quantize_store(k.numpy(), v.numpy(), cache, np.arange(S, dtype=np.int64), 1)
+    slots = cache[:, 0].transpose(1, 0, 2)                              # [KV, S, D+8]
+    kp, vp = slots[..., : D // 2].copy(), slots[..., D // 2: D].copy()
+    rul = np.ascontiguousarray(slots[..., D:]).view(np.float16)         # [KV, S, 4]
+    kmin, kstep, vmin, vstep = (np.ascontiguousarray(rul[..., i]) for i in range(4))
+    tens = [torch.from_numpy(a).to(DEV) for a in (kp, kmin, kstep, vp, vmin, vstep)]
+    out = _kd().kv_dequant_decode_per_token_attention(q.to(DEV), *tens, num_kv_heads=KV)
+    torch.cuda.synchronize()
+    ref = oa.decode_per_token(q.numpy(), kp, kmin, kstep, vp, vmin, vstep)
+    assert_close(out.cpu().numpy(), ref, what="per-token decode")
