@@ -1,0 +1,268 @@
+#!/usr/bin/env python3
+"""Benchmark of the batched paged 4-bit GQA decode attention on one MI355X.
+
+Workload (the headline configuration): one decode step of 64 sequences with
+lengths drawn uniformly from [512, 8192] (seed 0), 32 query / 8 KV heads,
+head_dim 128, block size 16, K/V ~ N(0, 1) quantized into the packed per-token
+min/step cache [num_blocks, 16, 8, 136] (uint8), block tables a random
+permutation of exactly the blocks needed.  A step is one launch of the fused
+dequant + attention over the whole batch; inputs are resident in HBM.  Three
+independent caches and queries (~303 MB of KV each, together above the 256 MB
+Infinity Cache) are rotated so no step is served from it.
+
+Printed: one JSON line with the throughput in algorithmic GB/s (packed KV +
+rulers, q, fp32 out, block-table entries and lengths actually read), the time
+per step, the roofline object for the decode kernel and a CPU baseline (the
+reference's CPU torch path on a bounded sample of the same workload).
+
+    python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _p in (ROOT / "slm-turbo_amd", ROOT):
+    if str(_p) not in sys.path:
+        sys.path.insert(0, str(_p))
+
+METRIC = "decode-attn µs/step + HBM GB/s (% of 8 TB/s), D=128 GQA paged 4-bit"
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E peak
+B, H, KV, D, BS = 64, 32, 8, 128, 16
+LEN_LO, LEN_HI = 512, 8192
+TRAFFIC_FILE = ROOT / "profiles" / "paged_decode_b64_h32_kv8_d128_traffic.txt"
+
+
+def parse_args(argv=None):
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--sets", type=int, default=3, help="independent cache/query sets rotated per step")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0, help="CPU baseline time budget")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--calibrate-copy-mb", type=int, default=0,
+                    help="also run a plain device copy of this many MB (counter calibration)")
+    return ap.parse_args(argv)
+
+
+def build_workload(seed: int, sets: int, dev):
+    import torch
+
+    from kernels import kv_dequant as kd
+
+    g = torch.Generator().manual_seed(seed)
+    lens = torch.randint(LEN_LO, LEN_HI + 1, (B,), generator=g)
+    nblk = (lens + BS - 1) // BS
+    total = int(nblk.sum())
+    perm = torch.randperm(total, generator=g)
+    maxb = int(nblk.max())
+    tables = torch.zeros((B, maxb), dtype=torch.int32)
+    off = 0
+    for b in range(B):
+        n = int(nblk[b])
+        tables[b, :n] = perm[off:off + n].to(torch.int32)
+        off += n
+    # flat slot of every token of every sequence
+    slot_chunks = []
+    for b in range(B):
+        pos = torch.arange(int(lens[b]))
+        slot_chunks.append(tables[b, pos // BS].long() * BS + pos % BS)
+    slots = torch.cat(slot_chunks).to(dev)
+    N = slots.numel()
+    qs, caches = [], []
+    for s in range(sets):
+        qs.append(torch.randn((B, H, D), generator=g).half().to(dev))
+        cache = torch.empty((total, BS, KV, D + 8), dtype=torch.uint8, device=dev)
+        gg = torch.Generator(device=dev).manual_seed(seed * 1000 + s)
+        chunk = 1 << 16
+        for t0 in range(0, N, chunk):
+            n = min(chunk, N - t0)
+            k = torch.randn((n, KV, D), generator=gg, device=dev).half()
+            v = torch.randn((n, KV, D), generator=gg, device=dev).half()
+            kd.kv_quantize_store(k, v, cache, slots[t0:t0 + n], BS)
+        caches.append(cache)
+    torch.cuda.synchronize()
+    return lens, tables, qs, caches
+
+
+def algorithmic_bytes(lens) -> int:
+    """Bytes a perfect kernel must move per step: packed KV + rulers of every
+    token, q (fp16), out (fp32), the block-table entries used and the lengths."""
+    L = [int(x) for x in lens]
+    blocks = sum((x + BS - 1) // BS for x in L)
+    return sum(L) * KV * (D + 8) + B * H * D * 2 + B * H * D * 4 + blocks * 4 + B * 4
+
+
+def read_traffic():
+    """HBM bytes per launch measured with rocprofv3 counters (committed summary)."""
+    if not TRAFFIC_FILE.exists():
+        return None
+    for line in TRAFFIC_FILE.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch:"):
+            return int(float(line.split(":", 1)[1]))
+    return None
+
+
+def cpu_baseline(lens, tables, q, cache_gpu, out_gpu, budget_s: float):
+    """The reference's CPU torch path (oracle/cpu_path.py) on a bounded sample."""
+    import torch
+
+    from oracle import cpu_path
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    cache = cache_gpu.cpu()
+    qc = q.cpu()
+    # grow the sample (sequences in order) until one pass takes ~budget/4
+    seqs, t_one = [0], 0.0
+    cpu_path.paged_decode(qc, cache, tables, lens, BS, KV, seqs=[0])          # warm-up
+    while True:
+        t0 = time.perf_counter()
+        out = cpu_path.paged_decode(qc, cache, tables, lens, BS, KV, seqs=seqs)
+        t_one = time.perf_counter() - t0
+        if t_one >= budget_s / 4 or len(seqs) == B:
+            break
+        seqs = list(range(min(B, len(seqs) * 2)))
+    times = [t_one]
+    while sum(times) < budget_s * 0.75 and len(times) < 10:
+        t0 = time.perf_counter()
+        out = cpu_path.paged_decode(qc, cache, tables, lens, BS, KV, seqs=seqs)
+        times.append(time.perf_counter() - t0)
+    t = statistics.median(times)
+    L = [int(lens[b]) for b in seqs]
+    nbytes = sum(L) * KV * (D + 8) + len(seqs) * (H * D * 6 + 4) + sum((x + BS - 1) // BS for x in L) * 4
+    err = float((out[seqs] - out_gpu.cpu()[seqs]).abs().max())
+    return {
+        "value": round(nbytes / t / 1e9, 3),
+        "unit": "GB/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": f"{len(seqs)} of {B} sequences ({sum(L)} tokens), median of {len(times)} runs, "
+                  f"{t * 1e3:.1f} ms/run; fp32 SDPA after fp16-rounded dequant",
+        "us_per_sample_step": round(t * 1e6, 1),
+        "cpu_model": platform.processor() or platform.machine(),
+        "max_abs_diff_vs_gpu": err,
+    }
+
+
+def main(argv=None) -> int:
+    args = parse_args(argv)
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py: this build measures one GPU only (the decode path has no cross-GPU "
+              f"exchange); asked for --gpus {args.gpus} / WORLD_SIZE {world}.", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from kernels import _native
+    from kernels import kv_dequant as kd
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    lens, tables, qs, caches = build_workload(args.seed, args.sets, dev)
+    tables_d = tables.to(dev)
+    lens_d = lens.to(torch.int32).to(dev)
+    nb = caches[0].shape[0]
+    out = torch.empty((B, H, D), dtype=torch.float32, device=dev)
+
+    # correctness of the launch path (Python API) before timing
+    ref_out = kd.kv_dequant_decode_paged_batched(qs[0], caches[0], tables_d, lens_d, BS, KV)
+
+    lib = _native.load()
+    ws, ws_bytes = kd._workspace(lib, dev, B, H, KV, D)
+    stream = torch.cuda.current_stream(dev)
+    fn = lib.slmt_decode_paged
+    argsets = [(q.data_ptr(), H * D, D, c.data_ptr(), nb, BS, tables_d.data_ptr(), 32, tables_d.stride(0),
+                lens_d.data_ptr(), 0, B, H, KV, D, out.data_ptr(), _native.OUT_F32, H * D, D, ws, ws_bytes,
+                stream.cuda_stream) for q, c in zip(qs, caches)]
+
+    if args.calibrate_copy_mb:
+        n = args.calibrate_copy_mb << 20
+        src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        print(f"calibration copy: {n} bytes read, {n} bytes written", file=sys.stderr)
+
+    for i in range(args.warmup):
+        _native.check(lib, fn(*argsets[i % args.sets]))
+    torch.cuda.synchronize()
+
+    K = args.steps
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(K)]
+    t_start, t_end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()                     # single process: the barrier is this sync
+    t_start.record(stream)
+    for i in range(K):
+        ev[i][0].record(stream)
+        fn(*argsets[i % args.sets])
+        ev[i][1].record(stream)
+    t_end.record(stream)
+    torch.cuda.synchronize()
+    total_ms = t_start.elapsed_time(t_end)
+    launch_us = sorted(a.elapsed_time(b) * 1e3 for a, b in ev)
+
+    nbytes = algorithmic_bytes(lens)
+    ms_per_step = total_ms / K
+    value = nbytes / (ms_per_step * 1e-3) / 1e9
+    mean_launch = statistics.fmean(launch_us)
+    achieved = nbytes / (mean_launch * 1e-6) / 1e9
+    result = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "us_per_step": round(ms_per_step * 1e3, 2),
+        "pct_of_hbm_peak": round(100.0 * value / HBM_PEAK_GBS, 2),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int4 codes; int32 (QK) / fp32 (PV) accumulate",
+        "data": "synthetic: K,V ~ N(0,1) fp16 quantized into the packed cache; q ~ N(0,1)",
+        "config": {
+            "workload": "paged per-token 4-bit decode attention, batch 64, lengths U[512,8192] seed 0, "
+                        "32 q / 8 KV heads, head_dim 128, block 16",
+            "batch": B, "num_heads": H, "num_kv_heads": KV, "head_dim": D, "block_size": BS,
+            "total_tokens": int(lens.sum()), "algorithmic_bytes": nbytes,
+            "rotated_sets": args.sets, "out_dtype": "fp32",
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": read_traffic(),
+        },
+        "launch_us": {
+            "mean": round(mean_launch, 2),
+            "median": round(statistics.median(launch_us), 2),
+            "p10": round(launch_us[len(launch_us) // 10], 2),
+            "p90": round(launch_us[(9 * len(launch_us)) // 10], 2),
+        },
+    }
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_baseline(lens, tables, qs[0], caches[0], ref_out, args.cpu_seconds)
+    else:
+        result["cpu_baseline"] = None
+    print(json.dumps(result))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
