@@ -23,37 +23,65 @@ WsLayout ws_layout(const AttnPlan& pl, int B, int H, int D) {
   WsLayout w;
   w.counters = 0;
   w.part_o = kCounterCap * 4;
-  w.part_ml = w.part_o + al((int64_t)pl.W * 2 * H * D * 4);
-  w.total = w.part_ml + al((int64_t)pl.W * 2 * H * 2 * 4);
+  w.part_ml = w.part_o + al((int64_t)pl.W_ws * 2 * H * D * 4);
+  w.total = w.part_ml + al((int64_t)pl.W_ws * 2 * H * 2 * 4);
   (void)B;
   return w;
 }
 
 }  // namespace
 
-int plan_attention(int B, int H, int G, int D, AttnPlan* plan) {
+// Query heads per workgroup of a plan: all of them, at most 8 waves of 4.
+static int hpg_max(int H) {
+  const int h = ((H + 3) / 4) * 4;
+  return h < 4 * (attn::MAX_THREADS / 64) ? h : 4 * (attn::MAX_THREADS / 64);
+}
+
+int plan_attention(int B, int H, int G, int D, int dma_kv, AttnPlan* plan) {
   (void)B;
-  const size_t kBudget = 64 * 1024;   // leaves room for two workgroups per CU
-  int hpg = ((H + 3) / 4) * 4;
-  if (hpg > 4 * (attn::MAX_THREADS / 64)) hpg = 4 * (attn::MAX_THREADS / 64);
-  while (hpg > 4 && attn::lds_bytes_for(worst_nkv(hpg, G), D, hpg / 4) > kBudget) hpg -= 4;
-  const int waves = hpg / 4;
-  const size_t lds = attn::lds_bytes_for(worst_nkv(hpg, G), D, waves);
-  if (lds > 160 * 1024) return fail(SLMT_ERR_UNSUPPORTED, "attention: KV row too wide for LDS");
-  const int groups = (H + hpg - 1) / hpg;
   const int cus = device_cu_count();
   if (cus <= 0) return fail(SLMT_ERR_HIP, "attention: could not query the device");
-  int per_cu = 8 / waves;                           // up to 256 VGPRs per lane -> 8 waves per CU
-  const int by_lds = (int)((160 * 1024) / lds);
-  per_cu = per_cu < by_lds ? per_cu : by_lds;
-  if (per_cu < 1) per_cu = 1;
-  int W = cus * per_cu / groups;
-  if (W < 1) W = 1;
+  // Register-staged plan: up to 32 heads (8 waves) per group, LDS kept small
+  // enough for two workgroups per CU when the waves allow it.
+  const size_t kBudget = 64 * 1024;
+  int hpg = hpg_max(H);
+  while (hpg > 4 && (size_t)attn::lds_geom(worst_nkv(hpg, G), D, hpg / 4).total > kBudget) hpg -= 4;
+  int waves = hpg / 4;
+  size_t lds = attn::lds_geom(worst_nkv(hpg, G), D, waves).total;
+  if (lds > 160 * 1024) return fail(SLMT_ERR_UNSUPPORTED, "attention: KV row too wide for LDS");
+  int groups = (H + hpg - 1) / hpg;
+  auto workgroups = [&](size_t lds_b, int wv, int grp) {
+    int per_cu = 8 / wv;                            // up to 256 VGPRs per lane -> 8 waves per CU
+    const int by_lds = (int)((160 * 1024) / lds_b);
+    per_cu = per_cu < by_lds ? per_cu : by_lds;
+    if (per_cu < 1) per_cu = 1;
+    const int W = cus * per_cu / grp;
+    return W < 1 ? 1 : W;
+  };
   plan->heads_per_group = hpg;
   plan->groups = groups;
   plan->waves = waves;
-  plan->W = W;
+  plan->W = workgroups(lds, waves, groups);
+  plan->W_ws = plan->W;
+  plan->dma = false;
   plan->lds_bytes = lds;
+  if (dma_kv <= 0) return SLMT_OK;
+
+  // Direct-load plan: every wave's 4 heads share one KV head (G % 4 == 0) and
+  // cache rows are a multiple of 16 bytes (an even number of KV heads), so a
+  // wave's widened KV slot stays in its row.
+  if (G % 4 != 0 || ((int64_t)dma_kv * (D + 8)) % 16 != 0) return SLMT_OK;
+  const int dh = hpg_max(H);
+  const int dwaves = dh / 4;
+  const attn::DmaGeom geo = attn::dma_geom(D, dwaves);
+  if (geo.total > 160 * 1024) return SLMT_OK;
+  plan->heads_per_group = dh;
+  plan->groups = (H + dh - 1) / dh;
+  plan->waves = dwaves;
+  plan->W = workgroups((size_t)geo.total, dwaves, plan->groups);
+  plan->dma = true;
+  plan->lds_bytes = (size_t)geo.total;
+  if (plan->W > plan->W_ws) plan->W_ws = plan->W;
   return SLMT_OK;
 }
 
@@ -63,7 +91,7 @@ int64_t attention_workspace_bytes(int B, int H, int KV, int D) {
     return -1;
   }
   AttnPlan pl;
-  if (plan_attention(B, H, H / KV, D, &pl) != SLMT_OK) return -1;
+  if (plan_attention(B, H, H / KV, D, KV, &pl) != SLMT_OK) return -1;
   if ((int64_t)pl.groups * B > kCounterCap) {
     fail(SLMT_ERR_UNSUPPORTED, "attention: more than 2^20 (sequence, head group) pairs in one call");
     return -1;
@@ -72,8 +100,14 @@ int64_t attention_workspace_bytes(int B, int H, int KV, int D) {
 }
 
 int launch_attention(int mode, int D, AttnParams& p, void* workspace, int64_t ws_bytes, hipStream_t stream) {
+  // Direct loads need a power-of-two block of at least 16 tokens (a tile is
+  // then one run of consecutive slots) and a 16-byte aligned cache.
+  const bool dma_ok = mode == SRC_PAGED && p.block_shift >= 4 && p.num_blocks < (int64_t(1) << 31) &&
+                      (reinterpret_cast<uintptr_t>(p.cache) & 15) == 0 &&
+                      (reinterpret_cast<uintptr_t>(p.q) & 15) == 0 && p.q_seq_stride % 8 == 0 &&
+                      p.q_head_stride % 8 == 0 && ((int64_t)p.H * p.q_head_stride + D) * 2 < (int64_t(1) << 31);
   AttnPlan pl;
-  int rc = plan_attention(p.B, p.H, p.G, D, &pl);
+  int rc = plan_attention(p.B, p.H, p.G, D, dma_ok ? p.cache_kv : 0, &pl);
   if (rc != SLMT_OK) return rc;
   if ((int64_t)pl.groups * p.B > kCounterCap)
     return fail(SLMT_ERR_UNSUPPORTED, "attention: more than 2^20 (sequence, head group) pairs in one call");
@@ -87,13 +121,12 @@ int launch_attention(int mode, int D, AttnParams& p, void* workspace, int64_t ws
   p.counters = reinterpret_cast<int*>(ws + lay.counters);
   p.heads_per_group = pl.heads_per_group;
   p.W = pl.W;
+  p.nthreads = pl.waves * 64;
   if (p.min_tiles <= 0) p.min_tiles = 4;
   const dim3 grid(pl.W, pl.groups), block(pl.waves * 64);
   if (mode == SRC_PAGED) {
     const bool shared = (p.G % 4) == 0;   // every wave's 4 heads share one KV head
-    // contiguous tiles: 16 | block_size and one group covering the whole cache row
-    const bool fast = p.block_shift >= 4 && pl.groups == 1 && ((int64_t)p.cache_kv * (D + 8)) % 8 == 0;
-    return launch_attention_paged(D, shared, fast, p, grid, block, pl.lds_bytes, stream);
+    return launch_attention_paged(D, shared, pl.dma, p, grid, block, pl.lds_bytes, stream);
   }
   return launch_attention_contig(mode, D, p, grid, block, pl.lds_bytes, stream);
 }

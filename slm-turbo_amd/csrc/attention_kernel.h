@@ -15,11 +15,19 @@
 //   sequence, whole sequences and the start of another.  A sequence split
 //   over several workgroups is merged by the last workgroup to finish its
 //   piece (log-sum-exp merge of (m, l, o) partials; arrival counter per
-//   sequence), so one launch produces the final output.
-// * Staging: each tile (16 tokens x the workgroup's KV heads) is copied into
-//   LDS with coalesced 8-byte loads, double-buffered; the next tile's loads
-//   are in flight (in registers) while the current tile is computed.  Tile
-//   barriers fence LDS only, so those loads stay in flight across them.
+//   sequence), so one launch produces the final output.  Arrivals are
+//   counted once the workgroup has finished its whole range, so the load
+//   pipeline never drains in the middle of it.
+// * Staging, paged fast path: a tile (16 tokens x every KV head) is one
+//   contiguous byte range of the cache.  It is copied straight into LDS with
+//   16-byte direct loads (global_load_lds_dwordx4, no VGPRs) into a ring of
+//   NSTAGE buffers, so NSTAGE-1 tiles are in flight while one is computed.
+//   Each wave waits for its own direct loads with an exact vmcnt and a
+//   workgroup barrier publishes the tile.  The query of a sequence rides in
+//   the same ring (one more direct load per wave), block-table entries and
+//   lengths are scalar loads fetched a tile ahead.
+// * Staging, general path (other layouts): the next tile's 8-byte chunks are
+//   held in registers while the current one is computed, double-buffered.
 // * QK (lane = token p x query head g of the wave's 4 heads): the query is
 //   quantized once per sequence to 16-bit fixed point and split into four
 //   4-bit limbs; v_dot8_u32_u4 multiplies 8 packed key nibbles by 8 limb
@@ -29,10 +37,11 @@
 // * Softmax: online, base 2 (log2(e)/sqrt(D) folded into the score scale),
 //   per-tile max via DPP row rotations and permlane16/32 swaps.
 // * PV (lane = packed byte j, i.e. dims 2j and 2j+1, for all 4 heads):
-//   v_dot2c_f32_f16 over token pairs.  The 16-bit halves of the operand are
-//   the masked nibbles themselves read as fp16 subnormals (n * 2^-24), which
-//   the instruction multiplies exactly, so unpacking a V byte pair costs one
-//   AND per dim.  Weights are p * step in fp16; accumulation is fp32; the
+//   v_dot2c_f32_f16 over token pairs.  The two tokens' bytes are packed into
+//   one dword (bytes at bits 0 and 16) and read as an fp16 pair of
+//   subnormals, (lo + 16 hi) * 2^-24, which the instruction multiplies
+//   exactly; a second product with the low nibbles alone (one AND) separates
+//   the two dims.  Weights are p * step in fp16; accumulation is fp32; the
 //   per-token min enters once per token as sum(p * min).
 #pragma once
 
@@ -43,10 +52,13 @@
 namespace slmt {
 namespace attn {
 
-constexpr int TILE = 16;
-constexpr int WSCR = 1024;        // per-wave LDS scratch bytes (query limbs / weights)
+constexpr int TILE = 16;           // tokens per tile, register-staged path
+constexpr int DTILE = 32;          // tokens per tile, direct-load path
+constexpr int WSCR = 1024;         // per-wave LDS scratch bytes (query limbs / weights)
 constexpr int MAX_THREADS = 512;   // 8 waves: up to 256 VGPRs per wave
-constexpr int MAXP = 5;           // 8-byte chunks prefetched per thread
+constexpr int MAXP = 5;            // 8-byte chunks prefetched per thread (general path)
+constexpr int DSTAGE = 3;          // LDS ring depth of the direct-load path
+constexpr int QSLOT = 1024;        // LDS bytes of one wave's query rows in a ring slot
 
 __device__ __forceinline__ float readlane_f(float x, int l) {
   return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), l));
@@ -71,12 +83,82 @@ __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
 }
 
+// Direct-load pipeline wait: until at most N of this wave's vector memory
+// operations are outstanding.  Its direct loads retire in issue order, so
+// every load older than the newest N has landed in LDS.  The asm is a
+// compiler memory barrier: no LDS access moves across it.
+template <int N>
+__device__ __forceinline__ void vm_wait_n() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+// Wait until tile t's loads have landed when `ahead` later tiles (OPS loads
+// each, plus possibly query loads) have been issued after it: at most
+// OPS * ahead operations may still be outstanding.  Extra later operations
+// only make the wait stricter.
+template <int OPS>
+__device__ __forceinline__ void vm_wait_tiles(int ahead) {   // ahead wave-uniform, 0 .. DSTAGE-2
+  static_assert(DSTAGE == 3, "one case per possible look-ahead");
+  if (ahead >= 1) vm_wait_n<OPS>();
+  else vm_wait_n<0>();
+}
+
+// One 16-byte direct load per lane: global (sbase + voff) -> LDS byte address
+// lds + 16 * lane.  Issued from asm so that the compiler's wait insertion
+// does not treat every later LDS read as a possible alias of the load (it
+// would wait for all of them); completion is tracked by vm_wait_barrier.
+// M0 carries the LDS base; nothing else in these kernels uses M0.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void lds_load16(const void* sbase, uint32_t voff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(lds)
+               : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+// Partial results cross workgroups (and XCDs) through the workspace.  They
+// are written and read with relaxed agent-scope atomics, which the hardware
+// performs coherently at device scope (write-through / past the per-XCD L2),
+// so publishing them needs only a wait for the stores to complete -- no L2
+// write-back or invalidate, which a release/acquire fence would issue.
+__device__ __forceinline__ void store_pair_agent(float* dst, float a, float b) {
+  const uint64_t v = (uint64_t)__builtin_bit_cast(uint32_t, a) | ((uint64_t)__builtin_bit_cast(uint32_t, b) << 32);
+  __hip_atomic_store(reinterpret_cast<uint64_t*>(dst), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float2 load_pair_agent(const float* src) {
+  const uint64_t v = __hip_atomic_load(reinterpret_cast<const uint64_t*>(src), __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+  return make_float2(__builtin_bit_cast(float, (uint32_t)v), __builtin_bit_cast(float, (uint32_t)(v >> 32)));
+}
+// Wait for all of this wave's vector memory operations (the agent-scope
+// partial stores among them) to complete.
+__device__ __forceinline__ void vm_drain() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// Scalar (SMEM) loads of wave-uniform table entries.  Reading through the
+// constant address space makes the compiler use s_load, which is counted by
+// lgkmcnt and so never waits on the vector loads that stream the cache.
+typedef const __attribute__((address_space(4))) int32_t c_i32;
+typedef const __attribute__((address_space(4))) int64_t c_i64;
+__device__ __forceinline__ int32_t sload_i32(const void* base, int64_t idx) {
+  return ((c_i32*)base)[idx];
+}
+__device__ __forceinline__ int64_t sload_i64(const void* base, int64_t idx) {
+  return ((c_i64*)base)[idx];
+}
+
+// Length of sequence b; `b` must be wave-uniform (scalar load).
 __device__ __forceinline__ int seq_len_of(const AttnParams& p, int b) {
+  if (b >= p.B) return 0;
+  int L = p.seq_lens ? sload_i32(p.seq_lens, b) : (p.causal_rows ? min(p.fixed_len, b + 1) : p.fixed_len);
+  return L < 0 ? 0 : L;
+}
+// Same for a per-lane b (vector load).
+__device__ __forceinline__ int seq_len_lane(const AttnParams& p, int b) {
   if (b >= p.B) return 0;
   int L = p.seq_lens ? p.seq_lens[b] : (p.causal_rows ? min(p.fixed_len, b + 1) : p.fixed_len);
   return L < 0 ? 0 : L;
 }
-__device__ __forceinline__ int tiles_of(int L) { return (L + TILE - 1) / TILE; }
+template <int TT>
+__device__ __forceinline__ int tiles_of(int L) { return (L + TT - 1) / TT; }
 
 // First tile of workgroup w when T tiles are split over Weff workgroups.
 __device__ __forceinline__ int range_start(int w, int T, int Weff) {
@@ -87,31 +169,47 @@ __device__ __forceinline__ int range_owner(int t, int T, int Weff) {
   return (int)((((long long)t + 1) * Weff - 1) / T);
 }
 
+// Walks the concatenated tile list.  Lnext, the length of sequence b+1, is
+// loaded when the cursor enters b, so crossing into b+1 does not wait on it.
 struct Cursor {
   int b, tb, Tb, Lb, Pb;   // sequence, tile in sequence, tiles/length of b, first global tile of b
+  int Lnext;
 };
 
+template <int TT>
 __device__ __forceinline__ void cursor_next(const AttnParams& p, Cursor& c) {
   c.tb++;
   if (c.tb >= c.Tb) {
     c.Pb += c.Tb;
     c.tb = 0;
-    do {
+    c.b++;
+    c.Lb = c.Lnext;
+    c.Tb = tiles_of<TT>(c.Lb);
+    while (c.Tb == 0 && c.b < p.B) {
       c.b++;
       c.Lb = seq_len_of(p, c.b);
-      c.Tb = tiles_of(c.Lb);
-    } while (c.Tb == 0 && c.b < p.B);
+      c.Tb = tiles_of<TT>(c.Lb);
+    }
+    c.Lnext = seq_len_of(p, c.b + 1);
   }
 }
 
+// Physical block of logical block idx of sequence b (wave-uniform arguments).
 __device__ __forceinline__ int64_t block_of(const AttnParams& p, int b, int idx) {
-  if (p.bt64) return reinterpret_cast<const int64_t*>(p.block_tables)[(int64_t)b * p.bt_stride + idx];
-  return reinterpret_cast<const int32_t*>(p.block_tables)[(int64_t)b * p.bt_stride + idx];
+  const int64_t e = (int64_t)b * p.bt_stride + idx;
+  if (p.bt64) return sload_i64(p.block_tables, e);
+  return sload_i32(p.block_tables, e);
+}
+// Same for a per-lane block index (vector load).
+__device__ __forceinline__ int64_t block_of_lane(const AttnParams& p, int b, int idx) {
+  const int64_t e = (int64_t)b * p.bt_stride + idx;
+  if (p.bt64) return reinterpret_cast<const int64_t*>(p.block_tables)[e];
+  return reinterpret_cast<const int32_t*>(p.block_tables)[e];
 }
 
-// Tile loader: chunk c of a tile is 8 bytes; a thread owns chunks tid + k*NT.
-// The first MAXP chunks of a thread are prefetched into registers; further
-// chunks (very wide rows) are copied at commit time.
+// Tile loader of the general path: chunk c of a tile is 8 bytes; a thread
+// owns chunks tid + k*NT.  The first MAXP chunks of a thread are prefetched
+// into registers; further chunks (very wide rows) are copied at commit time.
 template <int D, int MODE>
 struct Loader {
   static constexpr int SLOT = D + 8;
@@ -142,7 +240,7 @@ struct Loader {
           blk = tok / p.block_size;
           pos = tok - blk * p.block_size;
         }
-        const int64_t phys = block_of(p, b, (int)blk);
+        const int64_t phys = block_of_lane(p, b, (int)blk);
         const uint8_t* src = p.cache + ((phys * p.block_size + pos) * p.cache_kv + kv_lo) * (int64_t)SLOT +
                              (int64_t)ci * 8;
         v = *reinterpret_cast<const uint2*>(src);
@@ -168,11 +266,11 @@ struct Loader {
     return v;
   }
 
-  __device__ void issue(const AttnParams& p, int total, int cpr, int row_lds, int kv_lo, int b, int tok0,
+  __device__ void issue(const AttnParams& p, int NT, int total, int cpr, int row_lds, int kv_lo, int b, int tok0,
                         int Lb) {
 #pragma unroll
     for (int k = 0; k < MAXP; ++k) {
-      const int c = threadIdx.x + k * blockDim.x;
+      const int c = (int)threadIdx.x + k * NT;
       dst[k] = -1;
       if (c < total) {
         bool ok;
@@ -183,12 +281,12 @@ struct Loader {
     }
   }
 
-  __device__ void commit(const AttnParams& p, uint8_t* stage, int total, int cpr, int row_lds, int kv_lo,
+  __device__ void commit(const AttnParams& p, int NT, uint8_t* stage, int total, int cpr, int row_lds, int kv_lo,
                          int b, int tok0, int Lb) {
 #pragma unroll
     for (int k = 0; k < MAXP; ++k)
       if (dst[k] >= 0) *reinterpret_cast<uint2*>(stage + dst[k]) = reg[k];
-    for (int c = threadIdx.x + MAXP * blockDim.x; c < total; c += blockDim.x) {
+    for (int c = (int)threadIdx.x + MAXP * NT; c < total; c += NT) {
       bool ok;
       int off;
       const uint2 v = fetch(p, c, cpr, row_lds, kv_lo, b, tok0, Lb, off, ok);
@@ -197,75 +295,323 @@ struct Loader {
   }
 };
 
-// Paged fast path (block_size a multiple of 16 and the workgroup covering
-// every KV head of the cache row): a tile is one contiguous byte range of the
-// cache, so chunk k of a thread is at tile_base + (tid + k*NT) * 8.  Rows past
-// the sequence end are still inside the tile's block and are loaded; the
-// compute masks them.
-template <int D>
-struct FastLoader {
-  uint2 reg[MAXP];
-  int dst[MAXP];    // LDS offset, or -1 when the thread has no k-th chunk
-  const uint2* base = nullptr;   // tile base of the last issue (uniform)
-  int total = 0, cpr = 1, row_lds = 0;
-
-  __device__ void init(int total_, int cpr_, int row_lds_) {
-    total = total_;
-    cpr = cpr_;
-    row_lds = row_lds_;
-#pragma unroll
-    for (int k = 0; k < MAXP; ++k) {
-      const int c = threadIdx.x + k * blockDim.x;
-      const int r = c / cpr;
-      dst[k] = c < total ? r * row_lds + (c - r * cpr) * 8 : -1;
-    }
-  }
-
-  __device__ static const uint8_t* tile_base(const AttnParams& p, int b, int tok0) {
-    const int64_t phys = block_of(p, b, tok0 >> p.block_shift);
-    const int64_t slot0 = phys * p.block_size + (tok0 & (p.block_size - 1));
-    return p.cache + slot0 * p.cache_kv * (int64_t)(D + 8);
-  }
-
-  __device__ void issue(const AttnParams& p, int b, int tok0) {
-    base = reinterpret_cast<const uint2*>(tile_base(p, b, tok0));
-    const uint2* src = base + threadIdx.x;
-#pragma unroll
-    for (int k = 0; k < MAXP; ++k)
-      if (dst[k] >= 0) reg[k] = src[k * blockDim.x];
-  }
-
-  __device__ void commit(uint8_t* stage) {
-#pragma unroll
-    for (int k = 0; k < MAXP; ++k)
-      if (dst[k] >= 0) *reinterpret_cast<uint2*>(stage + dst[k]) = reg[k];
-    // chunks beyond MAXP per thread (small workgroups, wide rows): copy now
-    for (int c = threadIdx.x + MAXP * blockDim.x; c < total; c += blockDim.x) {
-      const int r = c / cpr;
-      *reinterpret_cast<uint2*>(stage + r * row_lds + (c - r * cpr) * 8) = base[c];
-    }
-  }
+// LDS geometry of a register-staged launch; the host computes the same
+// numbers for the dynamic LDS size.
+struct LdsGeom {
+  int row_bytes, row_lds, stage_bytes;
+  int wscr, misc, total;                  // byte offsets / total size
 };
 
-// SHARED: the 4 query heads of every wave read one KV head (G % 4 == 0),
-// so a V byte pair is unpacked once for all 4 heads.
-// FAST: paged tiles are contiguous (FastLoader); otherwise the general Loader.
-template <int D, int MODE, bool SHARED, bool FAST>
+__host__ __device__ inline LdsGeom lds_geom(int nkv, int D, int waves) {
+  LdsGeom g;
+  g.row_bytes = nkv * (D + 8);
+  // rows padded to an odd multiple of 8 bytes: conflict-free K reads
+  g.row_lds = g.row_bytes + ((g.row_bytes & 15) == 0 ? 8 : 0);
+  g.stage_bytes = (TILE * g.row_lds + 15) & ~15;
+  g.wscr = 2 * g.stage_bytes;
+  g.misc = g.wscr + waves * WSCR;
+  g.total = g.misc + 32 * (int)sizeof(int);
+  return g;
+}
+
+// Direct-load path (paged cache, the 4 query heads of every wave sharing one
+// KV head): a wave copies its KV head's slot of each of the tile's 32 cache
+// rows.  A slot is D+8 = 8 mod 16 bytes, so it starts 0 or 8 bytes into a
+// 16-byte unit and spans dma_units(D) units; with an even number of KV heads
+// (cache rows a multiple of 16 bytes) the widened slot never leaves its row.
+// Rows 0-15 and 16-31 of a tile are 16 consecutive slots of one block each;
+// the one load whose 64 units straddle the two halves is issued twice, each
+// time for the lanes of one half.
+__host__ __device__ constexpr int dma_units(int D) { return (D + 8 + 8 + 15) / 16; }
+__host__ __device__ constexpr int dma_ops(int D) { return (DTILE * dma_units(D) + 63) / 64; }
+__host__ __device__ constexpr int dma_split(int D) {   // load holding unit 16*units, or -1 if on a boundary
+  return (16 * dma_units(D)) % 64 ? (16 * dma_units(D)) / 64 : -1;
+}
+__host__ __device__ constexpr int dma_issues(int D) { return dma_ops(D) + (dma_split(D) >= 0 ? 1 : 0); }
+
+// Per-wave LDS region of the direct-load path: DSTAGE tile stages of
+// dma_ops(D) KB, DSTAGE query slots, the limb/weight scratch; misc follows
+// the last wave's region.
+struct DmaGeom {
+  int stage_bytes, wave_bytes, qslots, wscr, misc, total;
+};
+
+__host__ __device__ inline DmaGeom dma_geom(int D, int waves) {
+  DmaGeom g;
+  g.stage_bytes = dma_ops(D) * 1024;
+  g.qslots = DSTAGE * g.stage_bytes;
+  g.wscr = g.qslots + DSTAGE * QSLOT;
+  g.wave_bytes = g.wscr + WSCR;
+  g.misc = waves * g.wave_bytes;
+  g.total = g.misc + 32 * (int)sizeof(int);
+  return g;
+}
+
+// Per-lane state and per-tile math of one wave: 4 query heads of the
+// workgroup's head group, TOK (16 or 32) tokens per tile.  In QK a lane owns
+// query head g = lane & 3 and tokens p, p + 16, ... (p = lane >> 2).
+template <int D, int MODE, bool SHARED, int TOK>
+struct Heads {
+  static constexpr int SLOT = D + 8;
+  static constexpr int KD = D / 8;              // key dwords per token (8 dims each)
+  static constexpr int VB = D / 2;              // value bytes per token
+  static constexpr int NQ = TOK / 16;           // tokens per QK lane
+  static constexpr int PH = (D == 64) ? 2 : 1;  // PV token phases (two half-waves for D = 64)
+  static constexpr int PAIRS = TOK / 2 / PH;    // token pairs per PV lane per tile
+  static constexpr float kC = 1.4426950408889634f /
+      (D == 64 ? 8.0f : (D == 128 ? 11.313708498984761f : 8.94427190999916f));  // log2(e)/sqrt(D)
+
+  int qp, qg, hq, kvl, pj, pph, jj;
+  bool hvalid;
+  int kvw[4];
+  bool hw[4];
+  uint32_t ql[KD][4];
+  float qa, qb, m_run, l_run, vmt;
+  float acc[4][2];   // per head: sum w*lo, sum w*(lo + 16 hi), in units of 2^-24
+
+  __device__ void setup(int lane, int wave, int h0, int h1, int G, int kv_lo) {
+    qp = lane >> 2;
+    qg = lane & 3;
+    hq = h0 + wave * 4 + qg;
+    hvalid = hq < h1;
+    kvl = hvalid ? hq / G - kv_lo : 0;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int h = h0 + wave * 4 + g;
+      hw[g] = h < h1;
+      kvw[g] = hw[g] ? h / G - kv_lo : 0;
+    }
+    pj = (PH == 2) ? (lane & 31) : lane;
+    pph = (PH == 2) ? (lane >> 5) : 0;
+    jj = min(pj, VB - 1);
+  }
+
+  // Start a sequence: quantize the query (qv = this lane's 8 dims; for the
+  // per-channel layout already multiplied by k_scale, zv = k_zero) into limbs.
+  __device__ void begin(const float (&qv)[8], const float (&zv)[8], uint8_t* wscr) {
+    m_run = -INFINITY;
+    l_run = 0.f;
+    vmt = 0.f;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) acc[g][0] = acc[g][1] = 0.f;
+    float amax = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(qv[i]));
+    amax = red16_max(amax);
+    const float sq = amax > 0.f ? 32767.0f / amax : 1.0f;
+    // The score is computed exactly for the quantized query qi/sq: both the
+    // nibble dot and the ruler terms (sum q, sum q*zero) use qi, so the
+    // quantization error enters as sum(dq * K) with K the dequantized key.
+    uint32_t limb[4] = {0u, 0u, 0u, 0u};
+    int isum = 0;
+    float qzsum = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      int qi = (int)__builtin_rintf(qv[i] * sq);
+      qi = max(-32767, min(32767, qi));
+      isum += qi;
+      if constexpr (MODE == SRC_CHANNEL) qzsum += (float)qi * zv[i];
+      const uint32_t qu = (uint32_t)(qi + 32768);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) limb[k] |= ((qu >> (4 * k)) & 15u) << (4 * i);
+    }
+    const float qsum = red16_sum((float)isum) / sq;     // |sum qi| < 2^24: exact
+    float zsum = 0.f;
+    if constexpr (MODE == SRC_CHANNEL) zsum = red16_sum(qzsum) / sq;
+    uint32_t* wl = reinterpret_cast<uint32_t*>(wscr);
+    wave_lds_sync();                     // previous tile's weight reads are done
+    if (qp < KD) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) wl[(qg * 4 + k) * 16 + qp] = limb[k];
+    }
+    wave_lds_sync();
+#pragma unroll
+    for (int kd = 0; kd < KD; ++kd)
+#pragma unroll
+      for (int k = 0; k < 4; ++k) ql[kd][k] = wl[(qg * 4 + k) * 16 + kd];
+    qa = kC / sq;
+    if constexpr (MODE == SRC_CHANNEL) qb = -kC * zsum;
+    else qb = kC * qsum;
+  }
+
+  // Score of token row `row` of the tile for this lane's head (S_q * q.n
+  // folded with the rulers, base-2 units), and its V ruler for the weights.
+  __device__ float score(const uint8_t* S, int row_lds, int row, float& vmin, float& vstep) const {
+    const uint8_t* kb = S + row * row_lds + kvl * SLOT;
+    uint32_t a0 = 0, a1 = 0, a2 = 0, a3 = 0;
+#pragma unroll
+    for (int j = 0; j < KD / 2; ++j) {
+      const uint2 w = *reinterpret_cast<const uint2*>(kb + 8 * j);
+      a0 = __builtin_amdgcn_udot8(w.x, ql[2 * j][0], a0, false);
+      a1 = __builtin_amdgcn_udot8(w.x, ql[2 * j][1], a1, false);
+      a2 = __builtin_amdgcn_udot8(w.x, ql[2 * j][2], a2, false);
+      a3 = __builtin_amdgcn_udot8(w.x, ql[2 * j][3], a3, false);
+      a0 = __builtin_amdgcn_udot8(w.y, ql[2 * j + 1][0], a0, false);
+      a1 = __builtin_amdgcn_udot8(w.y, ql[2 * j + 1][1], a1, false);
+      a2 = __builtin_amdgcn_udot8(w.y, ql[2 * j + 1][2], a2, false);
+      a3 = __builtin_amdgcn_udot8(w.y, ql[2 * j + 1][3], a3, false);
+    }
+    // Nibble sum of the token.  When the wave's 4 heads share one KV head the
+    // 4 lanes of the token's quad read the same key, so each sums a quarter
+    // of its dwords and the quad adds the quarters; otherwise every lane sums
+    // its own key.
+    uint32_t sn = 0;
+    if constexpr (SHARED) {
+      const uint2 x0 = *reinterpret_cast<const uint2*>(kb + 16 * qg);
+      const uint2 x1 = *reinterpret_cast<const uint2*>(kb + 16 * qg + 8);
+      const uint32_t xs[4] = {x0.x, x0.y, x1.x, x1.y};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t ones = (KD >= 16 || 4 * qg + i < KD) ? 0x11111111u : 0u;   // key dwords only
+        sn = __builtin_amdgcn_udot8(xs[i], ones, sn, false);
+      }
+      sn += dpp_u<DPP_QUAD_XOR1>(sn);
+      sn += dpp_u<DPP_QUAD_XOR2>(sn);
+    } else {
+#pragma unroll
+      for (int j = 0; j < KD / 2; ++j) {
+        const uint2 w = *reinterpret_cast<const uint2*>(kb + 8 * j);
+        sn = __builtin_amdgcn_udot8(w.x, 0x11111111u, sn, false);
+        sn = __builtin_amdgcn_udot8(w.y, 0x11111111u, sn, false);
+      }
+    }
+    const int iacc = (int)(a0 + (a1 << 4) + (a2 << 8) + (a3 << 12)) - (int)(sn << 15);
+    const float x = (float)iacc;                 // = S_q * (q . n)
+    if constexpr (MODE == SRC_CHANNEL) {
+      vmin = vstep = 0.f;
+      return x * qa + qb;
+    } else {
+      const uint2 rr = *reinterpret_cast<const uint2*>(kb + D);
+      const float kmin = h2f((uint16_t)(rr.x & 0xffffu));
+      const float kstep = h2f((uint16_t)(rr.x >> 16));
+      vmin = h2f((uint16_t)(rr.y & 0xffffu));
+      vstep = h2f((uint16_t)(rr.y >> 16));
+      return (x * qa) * kstep + kmin * qb;
+    }
+  }
+
+  // One TOK-token tile staged at S (rows row_lds bytes apart, the staged KV
+  // heads side by side); tokens tok0 + p >= Lb are masked.
+  __device__ void tile(const uint8_t* S, int row_lds, int tok0, int Lb, uint8_t* wscr) {
+    // ---- QK
+    float s2[NQ], vmin[NQ], vstep[NQ];
+    bool tvalid[NQ];
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < NQ; ++i) {
+      s2[i] = score(S, row_lds, qp + 16 * i, vmin[i], vstep[i]);
+      tvalid[i] = hvalid && (tok0 + qp + 16 * i < Lb);
+      s2[i] = tvalid[i] ? s2[i] : -INFINITY;
+      tmax = fmaxf(tmax, s2[i]);
+    }
+    // ---- online softmax (running max per head; rescale only when it grows)
+    tmax = red16_max(tmax);
+    if (__builtin_amdgcn_ballot_w64(tmax > m_run)) {
+      const bool grow = tmax > m_run;
+      const float alpha = grow ? __builtin_amdgcn_exp2f(m_run - tmax) : 1.f;   // 0 when growing from -inf
+      const float m_new = grow ? tmax : m_run;
+      l_run *= alpha;
+      vmt *= alpha;
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const float ag = readlane_f(alpha, g);
+        acc[g][0] *= ag;
+        acc[g][1] *= ag;
+      }
+      m_run = m_new;
+    }
+    const float msafe = (m_run == -INFINITY) ? 0.f : m_run;
+    float wv[NQ];
+#pragma unroll
+    for (int i = 0; i < NQ; ++i) {
+      const float pr = __builtin_amdgcn_exp2f(s2[i] - msafe);
+      l_run += pr;
+      if constexpr (MODE == SRC_CHANNEL) {
+        wv[i] = pr;
+      } else {
+        wv[i] = tvalid[i] ? pr * vstep[i] : 0.f;
+        vmt += tvalid[i] ? pr * vmin[i] : 0.f;
+      }
+    }
+    // weights as fp16 pairs: wscr[pair][head] = (w(2i), w(2i+1))
+    wave_lds_sync();                     // limb / weight reads of this wave are done
+#pragma unroll
+    for (int i = 0; i < NQ; ++i)
+      reinterpret_cast<uint16_t*>(wscr)[(((qp + 16 * i) >> 1) * 4 + qg) * 2 + (qp & 1)] = f2h(wv[i]);
+    wave_lds_sync();
+    // ---- PV
+#pragma unroll
+    for (int i = 0; i < PAIRS; ++i) {
+      const int pr2 = pph * PAIRS + i;
+      const uint4 wq = *reinterpret_cast<const uint4*>(wscr + pr2 * 16);
+      if constexpr (SHARED) {
+        const uint8_t* vb = S + kvw[0] * SLOT + VB + jj;
+        const uint32_t tw = (uint32_t)vb[(2 * pr2) * row_lds] | ((uint32_t)vb[(2 * pr2 + 1) * row_lds] << 16);
+        const uint32_t vlo = tw & 0x000F000Fu;
+        acc[0][0] = fdot2(wq.x, vlo, acc[0][0]);
+        acc[0][1] = fdot2(wq.x, tw, acc[0][1]);
+        acc[1][0] = fdot2(wq.y, vlo, acc[1][0]);
+        acc[1][1] = fdot2(wq.y, tw, acc[1][1]);
+        acc[2][0] = fdot2(wq.z, vlo, acc[2][0]);
+        acc[2][1] = fdot2(wq.z, tw, acc[2][1]);
+        acc[3][0] = fdot2(wq.w, vlo, acc[3][0]);
+        acc[3][1] = fdot2(wq.w, tw, acc[3][1]);
+      } else {
+        const uint32_t wgs[4] = {wq.x, wq.y, wq.z, wq.w};
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const uint8_t* vb = S + kvw[g] * SLOT + VB + jj;
+          const uint32_t tw = (uint32_t)vb[(2 * pr2) * row_lds] | ((uint32_t)vb[(2 * pr2 + 1) * row_lds] << 16);
+          acc[g][0] = fdot2(wgs[g], tw & 0x000F000Fu, acc[g][0]);
+          acc[g][1] = fdot2(wgs[g], tw, acc[g][1]);
+        }
+      }
+    }
+  }
+
+  // End of a segment: lt/vt per head (lane g holds head g's values) and the
+  // un-normalized outputs o[g][0..1] of dims 2*pj, 2*pj+1 (valid in the
+  // writer lanes): o = sum p*(step*n) ... + sum p*min.
+  __device__ void reduce(float& lt, float& vt, float (&o)[4][2]) const {
+    lt = red16_sum(l_run);
+    vt = (MODE == SRC_CHANNEL) ? 0.f : red16_sum(vmt);
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      float lo = acc[g][0], full = acc[g][1];
+      if constexpr (PH == 2) {
+        float a, b2;
+        swap32(lo, a, b2);
+        lo = a + b2;
+        swap32(full, a, b2);
+        full = a + b2;
+      }
+      const float vg = readlane_f(vt, g);
+      o[g][0] = lo * 16777216.0f + vg;            // 2^24: nibble-as-subnormal scale
+      o[g][1] = (full - lo) * 1048576.0f + vg;    // (16 hi) * 2^-24 -> hi
+    }
+  }
+  __device__ bool writer() const { return (PH == 1 || pph == 0) && pj < VB; }
+};
+
+// DMA: paged cache, block_size a power of two >= 16, an even number of KV
+// heads (cache rows a multiple of 16 bytes) on a 16-byte aligned base, the 4
+// heads of every wave sharing a KV head (plan_attention and launch_attention
+// check).
+template <int D, int MODE, bool SHARED, bool DMA>
 __global__ void __launch_bounds__(MAX_THREADS) attention_kernel(const AttnParams p) {
-  constexpr int SLOT = D + 8;
-  constexpr int KD = D / 8;              // key dwords per token (8 dims each)
-  constexpr int VB = D / 2;              // value bytes per token
-  constexpr int PH = (D == 64) ? 2 : 1;  // PV token phases (two half-waves for D = 64)
-  constexpr int PAIRS = TILE / 2 / PH;   // token pairs per PV lane per tile
-  constexpr float kC = 1.4426950408889634f /
-                       (D == 64 ? 8.0f : (D == 128 ? 11.313708498984761f : 8.94427190999916f));  // log2(e)/sqrt(D)
+  constexpr int TT = DMA ? DTILE : TILE;   // tokens per tile
+  using HeadsT = Heads<D, MODE, SHARED, TT>;
+  static_assert(!DMA || SHARED, "direct loads copy one KV head per wave");
+  constexpr int KD = HeadsT::KD;
+  constexpr int VB = HeadsT::VB;
+  static_assert(!DMA || MODE == SRC_PAGED, "direct loads serve the paged layout only");
 
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int NT = blockDim.x;
+  const int wave = uniform(tid >> 6);
+  const int NT = p.nthreads;
   const int nwaves = NT >> 6;
   const int group = blockIdx.y;
   const int G = p.G;
@@ -273,19 +619,30 @@ __global__ void __launch_bounds__(MAX_THREADS) attention_kernel(const AttnParams
   const int h1 = min(p.H, h0 + p.heads_per_group);
   const int kv_lo = h0 / G;
   const int nkv = (h1 - 1) / G - kv_lo + 1;
-  const int row_bytes = nkv * SLOT;
-  const int row_lds = row_bytes + ((row_bytes & 15) == 0 ? 8 : 0);   // odd multiple of 8: conflict-free K reads
-  const int stage_bytes = (TILE * row_lds + 15) & ~15;
-  uint8_t* wscr = smem + 2 * stage_bytes + wave * WSCR;
-  // misc[0..16]: wave sums of the tile scan; misc[20..22]: broadcast slots
-  int* misc = reinterpret_cast<int*>(smem + 2 * stage_bytes + nwaves * WSCR);
+  // this wave's heads [hw0, hw1) (none for trailing waves of a short last group)
+  const int hw0 = h0 + 4 * wave;
+  const bool active = hw0 < h1;
+  const int hwa = active ? hw0 : h1 - 1;
+  const int hw1 = min(h1, hwa + 4);
+  const LdsGeom geo = lds_geom(nkv, D, nwaves);
+  const DmaGeom dgeo = dma_geom(D, nwaves);
+  constexpr int UNITS = dma_units(D), OPS = dma_ops(D), SPLIT = dma_split(D), ISSUES = dma_issues(D);
+  // direct-load path: this wave's KV head, its slot's place in the widened
+  // slice (kv_w * SLOT = a0 + koff) and the wave's LDS region
+  const int kv_w = hwa / G;
+  const int a0 = (kv_w * (D + 8)) & ~15, koff = kv_w * (D + 8) - a0;
+  uint8_t* const wbase = smem + wave * dgeo.wave_bytes;
+  const int row_lds = DMA ? UNITS * 16 : geo.row_lds;
+  uint8_t* wscr = DMA ? wbase + dgeo.wscr : smem + geo.wscr + wave * WSCR;
+  // misc[0..16]: wave sums of the tile scan; misc[20..27]: broadcast slots
+  int* misc = reinterpret_cast<int*>(smem + (DMA ? dgeo.misc : geo.misc));
 
   // ---------------------------------------------------------------- schedule
   // Exclusive scan of the per-sequence tile counts (threads own contiguous chunks).
   int T, my_excl, mysum = 0;
   const int chunk = (p.B + NT - 1) / NT;
   const int cb0 = min(p.B, tid * chunk), cb1 = min(p.B, cb0 + chunk);
-  for (int b = cb0; b < cb1; ++b) mysum += tiles_of(seq_len_of(p, b));
+  for (int b = cb0; b < cb1; ++b) mysum += tiles_of<TT>(seq_len_lane(p, b));
   {
     int v = mysum;
 #pragma unroll
@@ -331,7 +688,7 @@ __global__ void __launch_bounds__(MAX_THREADS) attention_kernel(const AttnParams
   if (lo >= my_excl && lo < my_excl + mysum) {
     int run = my_excl;
     for (int b = cb0; b < cb1; ++b) {
-      const int t = tiles_of(seq_len_of(p, b));
+      const int t = tiles_of<TT>(seq_len_lane(p, b));
       if (lo < run + t) {
         misc[20] = b;
         misc[21] = run;
@@ -345,371 +702,327 @@ __global__ void __launch_bounds__(MAX_THREADS) attention_kernel(const AttnParams
   cc.b = uniform(misc[20]);
   cc.Pb = uniform(misc[21]);
   cc.Lb = seq_len_of(p, cc.b);
-  cc.Tb = tiles_of(cc.Lb);
+  cc.Tb = tiles_of<TT>(cc.Lb);
   cc.tb = lo - cc.Pb;
-  Cursor lc = cc;                          // loader cursor runs one tile ahead
+  cc.Lnext = seq_len_of(p, cc.b + 1);
 
-  const int cpr = Loader<D, MODE>::chunks_per_row(nkv);
-  const int total_chunks = TILE * cpr;
+  HeadsT hd;
+  hd.setup(lane, wave, h0, h1, G, DMA ? kv_w : kv_lo);
 
-  // ---------------------------------------------------------------- lane roles
-  const int qp = lane >> 2;                // QK: token within the tile
-  const int qg = lane & 3;                 // QK: head slot within the wave
-  const int hq = h0 + wave * 4 + qg;
-  const bool hvalid = hq < h1;
-  const int kvl = hvalid ? hq / G - kv_lo : 0;
-  int kvw[4];                              // local kv row of each head of the wave (uniform)
-  bool hw[4];
+  // ---------------------------------------------------------------- loaders
+  // Direct loads: load k of this wave fills 1 KB of its stage; lane l of it
+  // moves 16-byte unit u = 64k + l of the wave's slice, tile row r = u / UNITS,
+  // column u % UNITS.  Rows 0-15 come from one block (base0), rows 16-31 from
+  // another (base1); tokens are cache_row bytes apart.  Units past the 32 rows
+  // re-read row 16's first unit into unused LDS.
+  const int cache_row = p.cache_kv * (D + 8);
+  uint32_t goff[OPS];
+  bool split_hi = false;                      // lane of load SPLIT belongs to rows 16-31
+  uint32_t qoff = 0;                          // this lane's query byte offset within a sequence
+  const uint32_t lds_wave = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)wbase;
+  if constexpr (DMA) {
 #pragma unroll
-  for (int g = 0; g < 4; ++g) {
-    const int h = h0 + wave * 4 + g;
-    hw[g] = h < h1;
-    kvw[g] = hw[g] ? h / G - kv_lo : 0;
+    for (int k = 0; k < OPS; ++k) {
+      const int u = 64 * k + lane;
+      const int r = u / UNITS, c = u - r * UNITS;
+      goff[k] = (uint32_t)(r < DTILE ? (r & 15) * cache_row + a0 + c * 16 : a0);
+      if (k == SPLIT) split_hi = r >= 16;
+    }
+    qoff = (hd.hvalid && hd.qp < KD) ? (uint32_t)((hd.hq * p.q_head_stride + hd.qp * 8) * 2) : 0u;
   }
-  const int pj = (PH == 2) ? (lane & 31) : lane;        // PV: byte index
-  const int pph = (PH == 2) ? (lane >> 5) : 0;          // PV: token phase
-  const int jj = min(pj, VB - 1);
+  // DMA: this wave's slice of the tile (rows 0-15 at base0, 16-31 at base1)
+  // into ring slot st, plus its query rows of sequence qb (qb >= 0) at a
+  // sequence start; exactly ISSUES (+1) loads per call.
+  const int64_t blk_bytes = (int64_t)p.block_size * cache_row;
+  auto dma_tile = [&](const uint8_t* base0, const uint8_t* base1, int st, int qb) {
+    if (!active) return;
+    const uint32_t dst = lds_wave + st * dgeo.stage_bytes;
+#pragma unroll
+    for (int k = 0; k < OPS; ++k) {
+      if (k == SPLIT) {
+        if (!split_hi) lds_load16(base0, goff[k], dst + k * 1024);
+        if (split_hi) lds_load16(base1, goff[k], dst + k * 1024);
+      } else {
+        lds_load16((64 * k) / UNITS < 16 ? base0 : base1, goff[k], dst + k * 1024);
+      }
+    }
+    if (qb >= 0) lds_load16(p.q + (int64_t)qb * p.q_seq_stride, qoff, lds_wave + dgeo.qslots + st * QSLOT);
+  };
 
-  // ---------------------------------------------------------------- prologue loads
-  using LoaderT = typename std::conditional<FAST, FastLoader<D>, Loader<D, MODE>>::type;
+  using LoaderT = Loader<D, MODE>;
   LoaderT ld;
-  auto issue = [&](const Cursor& c) {
-    if constexpr (FAST) ld.issue(p, c.b, c.tb * TILE);
-    else ld.issue(p, total_chunks, cpr, row_lds, kv_lo, c.b, c.tb * TILE, c.Lb);
-  };
-  auto commit = [&](const Cursor& c, uint8_t* stage) {
-    if constexpr (FAST) ld.commit(stage);
-    else ld.commit(p, stage, total_chunks, cpr, row_lds, kv_lo, c.b, c.tb * TILE, c.Lb);
-  };
-  if constexpr (FAST) ld.init(total_chunks, cpr, row_lds);
-  issue(lc);
-  commit(lc, smem);
-  if (lo + 1 < hi) {
-    cursor_next(p, lc);
-    issue(lc);
-  }
-  lds_barrier();
+  const int cpr = LoaderT::chunks_per_row(nkv);
+  const int total_chunks = TT * cpr;
 
-  // per-segment state
-  uint32_t ql[KD][4];
-  float qa = 0.f, qb = 0.f;
-  float m_run = -INFINITY, l_run = 0.f, vmt = 0.f;
-  float acc[4][2];
-  int seg_first_tile = lo;                 // global index of the segment's first tile
+  // Partial pieces whose arrival is counted after the range (at most two:
+  // the range's first and last segments): sequence, first tile, tiles.
+  int npend = 0;
+  int pb0 = 0, pP0 = 0, pT0 = 0, pb1 = 0, pP1 = 0, pT1 = 0;
 
-  for (int t = lo; t < hi; ++t) {
-    const int buf = (t - lo) & 1;
-    const uint8_t* S = smem + buf * stage_bytes;
-    const bool seg_start = (t == lo) || (cc.tb == 0);
-    const bool seg_end = (t == hi - 1) || (cc.tb == cc.Tb - 1);
-
-    // ------------------------------------------------------------ new sequence: query limbs
-    if (seg_start) {
-      seg_first_tile = t;
-      m_run = -INFINITY;
-      l_run = 0.f;
-      vmt = 0.f;
+  // Writes the finished segment [seg_first_tile, t] of sequence c.b.
+  auto finish_segment = [&](const Cursor& c, int seg_first_tile, int t) {
+    float lt, vt, o[4][2];
+    hd.reduce(lt, vt, o);
+    const bool complete = (seg_first_tile == c.Pb) && (t == c.Pb + c.Tb - 1);
+    const bool wr = hd.writer();
+    const int d0 = 2 * hd.pj;
+    if (complete) {
 #pragma unroll
-      for (int g = 0; g < 4; ++g) acc[g][0] = acc[g][1] = 0.f;
-      float qv[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) qv[i] = 0.f;
-      const bool dvalid = hvalid && (qp * 8 < D);
-      float zsum = 0.f;
-      float zv[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) zv[i] = 0.f;
-      if (dvalid) {
-        const uint16_t* qrow = p.q + (int64_t)cc.b * p.q_seq_stride + (int64_t)hq * p.q_head_stride + qp * 8;
-        const uint4 w = *reinterpret_cast<const uint4*>(qrow);
-        const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          qv[2 * i] = h2f((uint16_t)(ws[i] & 0xffffu));
-          qv[2 * i + 1] = h2f((uint16_t)(ws[i] >> 16));
-        }
+      for (int g = 0; g < 4; ++g) {
+        if (!hd.hw[g] || !wr) continue;
+        const int h = h0 + wave * 4 + g;
+        const float L = readlane_f(lt, g);
+        float r0 = o[g][0] / L, r1 = o[g][1] / L;
         if constexpr (MODE == SRC_CHANNEL) {
           if (p.use_quant) {
-            const int64_t kvg = kv_lo + kvl;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-              qv[i] *= h2f(p.kr0[kvg * D + qp * 8 + i]);          // q' = q * k_scale
-              zv[i] = h2f(p.kr1[kvg * D + qp * 8 + i]);           // k_zero
-            }
+            const int64_t kvg = h / G;
+            r0 = h2f(p.vr0[kvg * D + d0]) * (r0 - h2f(p.vr1[kvg * D + d0]));
+            r1 = h2f(p.vr0[kvg * D + d0 + 1]) * (r1 - h2f(p.vr1[kvg * D + d0 + 1]));
           }
         }
+        const int64_t off = (int64_t)c.b * p.out_seq_stride + (int64_t)h * p.out_head_stride + d0;
+        if (p.out_f16) {
+          *reinterpret_cast<uint32_t*>(reinterpret_cast<uint16_t*>(p.out) + off) =
+              (uint32_t)f2h(r0) | ((uint32_t)f2h(r1) << 16);
+        } else {
+          *reinterpret_cast<float2*>(reinterpret_cast<float*>(p.out) + off) = make_float2(r0, r1);
+        }
       }
-      float amax = 0.f;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(qv[i]));
-      amax = red16_max(amax);
-      const float sq = amax > 0.f ? 32767.0f / amax : 1.0f;
-      // The score is computed exactly for the quantized query qi/sq: both the
-      // nibble dot and the ruler terms (sum q, sum q*zero) use qi, so the
-      // quantization error enters as sum(dq * K) with K the dequantized key.
-      uint32_t limb[4] = {0u, 0u, 0u, 0u};
-      int isum = 0;
-      float qzsum = 0.f;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        int qi = (int)__builtin_rintf(qv[i] * sq);
-        qi = max(-32767, min(32767, qi));
-        isum += qi;
-        if constexpr (MODE == SRC_CHANNEL) qzsum += (float)qi * zv[i];
-        const uint32_t qu = (uint32_t)(qi + 32768);
-#pragma unroll
-        for (int k = 0; k < 4; ++k) limb[k] |= ((qu >> (4 * k)) & 15u) << (4 * i);
-      }
-      const float qsum = red16_sum((float)isum) / sq;     // |sum qi| < 2^24: exact
-      if constexpr (MODE == SRC_CHANNEL) zsum = red16_sum(qzsum) / sq;
-      uint32_t* wl = reinterpret_cast<uint32_t*>(wscr);
-      wave_lds_sync();                     // previous tile's weight reads are done
-      if (qp < KD) {
-#pragma unroll
-        for (int k = 0; k < 4; ++k) wl[(qg * 4 + k) * 16 + qp] = limb[k];
-      }
-      wave_lds_sync();
-#pragma unroll
-      for (int kd = 0; kd < KD; ++kd)
-#pragma unroll
-        for (int k = 0; k < 4; ++k) ql[kd][k] = wl[(qg * 4 + k) * 16 + kd];
-      qa = kC / sq;
-      if constexpr (MODE == SRC_CHANNEL) qb = -kC * zsum;
-      else qb = kC * qsum;
-    }
-
-    // ------------------------------------------------------------ QK
-    const int tok0 = cc.tb * TILE;
-    const uint8_t* kb = S + qp * row_lds + kvl * SLOT;
-    uint32_t a0 = 0, a1 = 0, a2 = 0, a3 = 0, sn = 0;
-#pragma unroll
-    for (int j = 0; j < KD / 2; ++j) {
-      const uint2 w = *reinterpret_cast<const uint2*>(kb + 8 * j);
-      a0 = __builtin_amdgcn_udot8(w.x, ql[2 * j][0], a0, false);
-      a1 = __builtin_amdgcn_udot8(w.x, ql[2 * j][1], a1, false);
-      a2 = __builtin_amdgcn_udot8(w.x, ql[2 * j][2], a2, false);
-      a3 = __builtin_amdgcn_udot8(w.x, ql[2 * j][3], a3, false);
-      a0 = __builtin_amdgcn_udot8(w.y, ql[2 * j + 1][0], a0, false);
-      a1 = __builtin_amdgcn_udot8(w.y, ql[2 * j + 1][1], a1, false);
-      a2 = __builtin_amdgcn_udot8(w.y, ql[2 * j + 1][2], a2, false);
-      a3 = __builtin_amdgcn_udot8(w.y, ql[2 * j + 1][3], a3, false);
-      sn = __builtin_amdgcn_udot8(w.x, 0x11111111u, sn, false);
-      sn = __builtin_amdgcn_udot8(w.y, 0x11111111u, sn, false);
-    }
-    const int iacc = (int)(a0 + (a1 << 4) + (a2 << 8) + (a3 << 12)) - (int)(sn << 15);
-    const float x = (float)iacc;                 // = S_q * (q . n)
-    const bool tvalid = hvalid && (tok0 + qp < cc.Lb);
-    float s2, wv, vmin = 0.f, vstep = 0.f;
-    if constexpr (MODE == SRC_CHANNEL) {
-      s2 = x * qa + qb;
     } else {
-      const uint2 rr = *reinterpret_cast<const uint2*>(kb + D);
-      const float kmin = h2f((uint16_t)(rr.x & 0xffffu));
-      const float kstep = h2f((uint16_t)(rr.x >> 16));
-      vmin = h2f((uint16_t)(rr.y & 0xffffu));
-      vstep = h2f((uint16_t)(rr.y >> 16));
-      s2 = (x * qa) * kstep + kmin * qb;
-    }
-    s2 = tvalid ? s2 : -INFINITY;
-    const float tmax = red16_max(s2);
-    const float m_new = fmaxf(m_run, tmax);
-    const float msafe = (m_new == -INFINITY) ? 0.f : m_new;
-    const float alpha = __builtin_amdgcn_exp2f(m_run - msafe);
-    const float pr = __builtin_amdgcn_exp2f(s2 - msafe);
-    l_run = l_run * alpha + pr;
-    if constexpr (MODE == SRC_CHANNEL) {
-      wv = pr;
-    } else {
-      wv = tvalid ? pr * vstep : 0.f;
-      vmt = vmt * alpha + (tvalid ? pr * vmin : 0.f);
-    }
-    m_run = m_new;
-    // weights as fp16 pairs: wscr[pair][head] = (w(2i), w(2i+1))
-    wave_lds_sync();                     // limb reads of this wave are done
-    reinterpret_cast<uint16_t*>(wscr)[((qp >> 1) * 4 + qg) * 2 + (qp & 1)] = f2h(wv);
-    // rescale the PV accumulators by each head's alpha (uniform per head)
-    float al[4];
-#pragma unroll
-    for (int g = 0; g < 4; ++g) al[g] = readlane_f(alpha, g);
-    if (al[0] != 1.f || al[1] != 1.f || al[2] != 1.f || al[3] != 1.f) {
+      // partial piece: slot 0 when this segment is the workgroup's first, else 1
+      const int slot = (seg_first_tile == lo) ? 0 : 1;
+      const int64_t pbase = ((int64_t)wg * 2 + slot) * p.H;
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        acc[g][0] *= al[g];
-        acc[g][1] *= al[g];
+        if (!hd.hw[g] || !wr) continue;
+        const int h = h0 + wave * 4 + g;
+        store_pair_agent(p.part_o + (pbase + h) * D + d0, o[g][0], o[g][1]);
+        if (hd.pj == 0) store_pair_agent(p.part_ml + (pbase + h) * 2, readlane_f(hd.m_run, g), readlane_f(lt, g));
       }
-    }
-    wave_lds_sync();
-
-    // ------------------------------------------------------------ PV
-#pragma unroll
-    for (int i = 0; i < PAIRS; ++i) {
-      const int pr2 = pph * PAIRS + i;
-      const uint4 wq = *reinterpret_cast<const uint4*>(wscr + pr2 * 16);
-      if constexpr (SHARED) {
-        const uint8_t* vb = S + kvw[0] * SLOT + VB + jj;
-        const uint32_t tw = (uint32_t)vb[(2 * pr2) * row_lds] | ((uint32_t)vb[(2 * pr2 + 1) * row_lds] << 16);
-        const uint32_t vlo = tw & 0x000F000Fu, vhi = tw & 0x00F000F0u;
-        acc[0][0] = fdot2(wq.x, vlo, acc[0][0]);
-        acc[0][1] = fdot2(wq.x, vhi, acc[0][1]);
-        acc[1][0] = fdot2(wq.y, vlo, acc[1][0]);
-        acc[1][1] = fdot2(wq.y, vhi, acc[1][1]);
-        acc[2][0] = fdot2(wq.z, vlo, acc[2][0]);
-        acc[2][1] = fdot2(wq.z, vhi, acc[2][1]);
-        acc[3][0] = fdot2(wq.w, vlo, acc[3][0]);
-        acc[3][1] = fdot2(wq.w, vhi, acc[3][1]);
+      if (npend == 0) {
+        pb0 = c.b;
+        pP0 = c.Pb;
+        pT0 = c.Tb;
       } else {
-        const uint32_t wgs[4] = {wq.x, wq.y, wq.z, wq.w};
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const uint8_t* vb = S + kvw[g] * SLOT + VB + jj;
-          const uint32_t tw = (uint32_t)vb[(2 * pr2) * row_lds] | ((uint32_t)vb[(2 * pr2 + 1) * row_lds] << 16);
-          acc[g][0] = fdot2(wgs[g], tw & 0x000F000Fu, acc[g][0]);
-          acc[g][1] = fdot2(wgs[g], tw & 0x00F000F0u, acc[g][1]);
-        }
+        pb1 = c.b;
+        pP1 = c.Pb;
+        pT1 = c.Tb;
       }
+      ++npend;
     }
+  };
 
-    // ------------------------------------------------------------ end of a segment
-    if (seg_end) {
-      const float lt = red16_sum(l_run);
-      const float vt = (MODE == SRC_CHANNEL) ? 0.f : red16_sum(vmt);
-      float o[4][2];
+  // Starts the segment of cursor c: query limbs from its 8 dims.
+  auto begin_segment = [&](const Cursor& c, const uint8_t* qlds) {
+    float qv[8], zv[8];
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        o[g][0] = acc[g][0];
-        o[g][1] = acc[g][1];
-        if constexpr (PH == 2) {
-          float a, b2;
-          swap32(o[g][0], a, b2);
-          o[g][0] = a + b2;
-          swap32(o[g][1], a, b2);
-          o[g][1] = a + b2;
-        }
-      }
-      const int Pb = cc.Pb, Tb = cc.Tb, b = cc.b;
-      const bool complete = (seg_first_tile == Pb) && (t == Pb + Tb - 1);
-      const bool writer = (PH == 1 || pph == 0) && pj < VB;
-      const int d0 = 2 * pj;
-      if (complete) {
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          if (!hw[g] || !writer) continue;
-          const int h = h0 + wave * 4 + g;
-          const float L = readlane_f(lt, g);
-          const float vg = readlane_f(vt, g);
-          const float n0 = o[g][0] * 16777216.0f + vg;   // 2^24: nibble-as-subnormal scale
-          const float n1 = o[g][1] * 1048576.0f + vg;    // 2^20: high nibble carried x16
-          float r0 = n0 / L, r1 = n1 / L;
-          if constexpr (MODE == SRC_CHANNEL) {
-            if (p.use_quant) {
-              const int64_t kvg = h / G;
-              r0 = h2f(p.vr0[kvg * D + d0]) * (r0 - h2f(p.vr1[kvg * D + d0]));
-              r1 = h2f(p.vr0[kvg * D + d0 + 1]) * (r1 - h2f(p.vr1[kvg * D + d0 + 1]));
-            }
-          }
-          const int64_t off = (int64_t)b * p.out_seq_stride + (int64_t)h * p.out_head_stride + d0;
-          if (p.out_f16) {
-            *reinterpret_cast<uint32_t*>(reinterpret_cast<uint16_t*>(p.out) + off) =
-                (uint32_t)f2h(r0) | ((uint32_t)f2h(r1) << 16);
-          } else {
-            *reinterpret_cast<float2*>(reinterpret_cast<float*>(p.out) + off) = make_float2(r0, r1);
-          }
-        }
+    for (int i = 0; i < 8; ++i) qv[i] = zv[i] = 0.f;
+    const bool dvalid = hd.hvalid && (hd.qp < KD);
+    if (dvalid) {
+      uint4 w;
+      if constexpr (DMA) {
+        w = *reinterpret_cast<const uint4*>(qlds + lane * 16);
       } else {
-        // partial piece: slot 0 when this segment is the workgroup's first, else 1
-        const int slot = (seg_first_tile == lo) ? 0 : 1;
-        const int64_t pbase = ((int64_t)wg * 2 + slot) * p.H;
+        const uint16_t* qrow =
+            p.q + (int64_t)c.b * p.q_seq_stride + (int64_t)hd.hq * p.q_head_stride + hd.qp * 8;
+        w = *reinterpret_cast<const uint4*>(qrow);
+      }
+      const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          if (!hw[g] || !writer) continue;
-          const int h = h0 + wave * 4 + g;
-          const float vg = readlane_f(vt, g);
-          const float n0 = o[g][0] * 16777216.0f + vg;
-          const float n1 = o[g][1] * 1048576.0f + vg;
-          *reinterpret_cast<float2*>(p.part_o + (pbase + h) * D + d0) = make_float2(n0, n1);
-          if (pj == 0) {
-            p.part_ml[(pbase + h) * 2] = readlane_f(m_run, g);
-            p.part_ml[(pbase + h) * 2 + 1] = readlane_f(lt, g);
+      for (int i = 0; i < 4; ++i) {
+        qv[2 * i] = h2f((uint16_t)(ws[i] & 0xffffu));
+        qv[2 * i + 1] = h2f((uint16_t)(ws[i] >> 16));
+      }
+      if constexpr (MODE == SRC_CHANNEL) {
+        if (p.use_quant) {
+          const int64_t kvg = kv_lo + hd.kvl;
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            qv[i] *= h2f(p.kr0[kvg * D + hd.qp * 8 + i]);          // q' = q * k_scale
+            zv[i] = h2f(p.kr1[kvg * D + hd.qp * 8 + i]);           // k_zero
           }
-        }
-        // arrival: the last piece of sequence b merges all pieces
-        const int w_first = range_owner(Pb, T, Weff);
-        const int w_last = range_owner(Pb + Tb - 1, T, Weff);
-        const int pieces = w_last - w_first + 1;
-        // Every wave publishes its own partial stores at agent scope (waits
-        // for them and writes back L2) before the arrival is counted: a
-        // barrier alone does not wait for other waves' stores, and the merge
-        // may run on another XCD.
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-        __syncthreads();
-        if (tid == 0) {
-          const int prev = __hip_atomic_fetch_add(p.counters + (int64_t)group * p.B + b, 1, __ATOMIC_ACQ_REL,
-                                                  __HIP_MEMORY_SCOPE_AGENT);
-          misc[22] = (prev == pieces - 1) ? 1 : 0;
-        }
-        __syncthreads();
-        if (misc[22]) {
-          __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-          const int first_slot = (range_start(w_first, T, Weff) == Pb) ? 0 : 1;
-          for (int e = tid; e < (h1 - h0) * D; e += NT) {
-            const int h = h0 + e / D, d = e - (e / D) * D;
-            float M = -INFINITY;
-            for (int w = w_first; w <= w_last; ++w) {
-              const int s = (w == w_first) ? first_slot : 0;
-              M = fmaxf(M, p.part_ml[(((int64_t)w * 2 + s) * p.H + h) * 2]);
-            }
-            float Lsum = 0.f, Osum = 0.f;
-            for (int w = w_first; w <= w_last; ++w) {
-              const int s = (w == w_first) ? first_slot : 0;
-              const int64_t base = ((int64_t)w * 2 + s) * p.H + h;
-              const float sc = __builtin_amdgcn_exp2f(p.part_ml[base * 2] - M);
-              Lsum += sc * p.part_ml[base * 2 + 1];
-              Osum += sc * p.part_o[base * D + d];
-            }
-            float r = Osum / Lsum;
-            if constexpr (MODE == SRC_CHANNEL) {
-              if (p.use_quant) {
-                const int64_t kvg = h / G;
-                r = h2f(p.vr0[kvg * D + d]) * (r - h2f(p.vr1[kvg * D + d]));
-              }
-            }
-            const int64_t off = (int64_t)b * p.out_seq_stride + (int64_t)h * p.out_head_stride + d;
-            if (p.out_f16) reinterpret_cast<uint16_t*>(p.out)[off] = f2h(r);
-            else reinterpret_cast<float*>(p.out)[off] = r;
-          }
-          if (tid == 0)
-            __hip_atomic_store(p.counters + (int64_t)group * p.B + b, 0, __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
         }
       }
     }
+    hd.begin(qv, zv, wscr);
+  };
 
-    // ------------------------------------------------------------ advance the pipeline
-    if (t + 1 < hi) {
-      cursor_next(p, cc);
-      // tile t+1 is in registers (issued by the loader cursor); commit it
-      commit(lc, smem + (buf ^ 1) * stage_bytes);
-      if (t + 2 < hi) {
-        cursor_next(p, lc);
-        issue(lc);
+  int seg_first_tile = lo;
+
+  if constexpr (DMA) {
+    // ---------------------------------------------------------------- direct-load pipeline
+    // Every wave runs its own ring of DSTAGE slots (no workgroup barriers):
+    // tiles lo .. lo+DSTAGE-2 are issued up front; iteration t waits for tile
+    // t, issues tile t+DSTAGE-1 into the slot tile t-1 used, computes tile t.
+    // The block-table entries of the next tile to issue are loaded one
+    // iteration early and kept raw until used, so their loads are not waited
+    // on where they are issued.  Entries are read as their low 32 bits
+    // (physical blocks are below 2^31: the host checks num_blocks), so 32-
+    // and 64-bit tables take the same path.
+    const int esh = p.bt64 ? 3 : 2;
+    const uint8_t* btab = reinterpret_cast<const uint8_t*>(p.block_tables);
+    auto entry_of = [&](int b, int tok) -> int32_t {
+      return sload_i32(btab + (((int64_t)b * p.bt_stride + (tok >> p.block_shift)) << esh), 0);
+    };
+    // slot base of token tok of a tile (rows of the same block follow)
+    auto slot_base = [&](int32_t phys, int tok) -> const uint8_t* {
+      return p.cache + (int64_t)phys * blk_bytes + (int64_t)(tok & (p.block_size - 1)) * cache_row;
+    };
+    Cursor dc = cc;
+    int32_t pf0 = 0, pf1 = 0;  // entries of the tile after dc (rows 0-15, 16-31) when pf_ok
+    bool pf_ok = false;
+    auto prefetch_after = [&](const Cursor& c) {
+      // tile following c: same sequence, or the first tile of sequence b+1
+      // when that one is not empty (else looked up at issue); the loads
+      // always go to valid entries so that nothing branches around them
+      const bool same = c.tb + 1 < c.Tb;
+      const bool next_ok = c.Lnext > 0 && c.b + 1 < p.B;
+      pf_ok = same || next_ok;
+      const int nb = same ? c.b : (next_ok ? c.b + 1 : c.b);
+      const int ntok = same ? (c.tb + 1) * DTILE : (next_ok ? 0 : c.tb * DTILE);
+      const int nL = same ? c.Lb : (next_ok ? c.Lnext : c.Lb);
+      pf0 = entry_of(nb, ntok);
+      pf1 = entry_of(nb, ntok + 16 < nL ? ntok + 16 : ntok);
+    };
+    auto issue = [&](const Cursor& c, bool use_pf, int st, int qb) {
+      const int tok0 = c.tb * DTILE;
+      const bool upper = tok0 + 16 < c.Lb;     // rows 16-31 hold tokens of the sequence
+      const int32_t e0 = use_pf ? pf0 : entry_of(c.b, tok0);
+      const int32_t e1 = use_pf ? pf1 : entry_of(c.b, upper ? tok0 + 16 : tok0);
+      const uint8_t* b0 = slot_base(e0, tok0);
+      dma_tile(b0, upper ? slot_base(e1, tok0 + 16) : b0, st, qb);
+    };
+    for (int j = 0; j < DSTAGE - 1 && lo + j < hi; ++j) {
+      if (j > 0) cursor_next<TT>(p, dc);
+      issue(dc, false, (lo + j) % DSTAGE, (j == 0 || dc.tb == 0) ? dc.b : -1);
+    }
+    prefetch_after(dc);
+    int st = lo % DSTAGE;                           // ring slot of tile t
+    for (int t = lo; t < hi; ++t) {
+      vm_wait_tiles<ISSUES>(min(DSTAGE - 2, hi - 1 - t));
+      if (t + DSTAGE - 1 < hi) {
+        cursor_next<TT>(p, dc);
+        issue(dc, pf_ok, st == 0 ? DSTAGE - 1 : st - 1, dc.tb == 0 ? dc.b : -1);
+        prefetch_after(dc);
       }
-      lds_barrier();
+      const bool seg_start = (t == lo) || (cc.tb == 0);
+      const bool seg_end = (t == hi - 1) || (cc.tb == cc.Tb - 1);
+      if (seg_start) {
+        seg_first_tile = t;
+        begin_segment(cc, wbase + dgeo.qslots + st * QSLOT);
+      }
+      hd.tile(wbase + st * dgeo.stage_bytes + koff, row_lds, cc.tb * TT, cc.Lb, wscr);
+      if (seg_end) finish_segment(cc, seg_first_tile, t);
+      if (t + 1 < hi) cursor_next<TT>(p, cc);
+      st = st + 1 == DSTAGE ? 0 : st + 1;
+    }
+  } else {
+    // ---------------------------------------------------------------- register-staged pipeline
+    Cursor lc = cc;                          // loader cursor runs one tile ahead
+    ld.issue(p, NT, total_chunks, cpr, row_lds, kv_lo, lc.b, lc.tb * TILE, lc.Lb);
+    ld.commit(p, NT, smem, total_chunks, cpr, row_lds, kv_lo, lc.b, lc.tb * TILE, lc.Lb);
+    if (lo + 1 < hi) {
+      cursor_next<TT>(p, lc);
+      ld.issue(p, NT, total_chunks, cpr, row_lds, kv_lo, lc.b, lc.tb * TILE, lc.Lb);
+    }
+    lds_barrier();
+    for (int t = lo; t < hi; ++t) {
+      const int buf = (t - lo) & 1;
+      const bool seg_start = (t == lo) || (cc.tb == 0);
+      const bool seg_end = (t == hi - 1) || (cc.tb == cc.Tb - 1);
+      if (seg_start) {
+        seg_first_tile = t;
+        begin_segment(cc, nullptr);
+      }
+      hd.tile(smem + buf * geo.stage_bytes, row_lds, cc.tb * TILE, cc.Lb, wscr);
+      if (seg_end) finish_segment(cc, seg_first_tile, t);
+      if (t + 1 < hi) {
+        cursor_next<TT>(p, cc);
+        // tile t+1 is in registers (issued by the loader cursor); commit it
+        ld.commit(p, NT, smem + (buf ^ 1) * geo.stage_bytes, total_chunks, cpr, row_lds, kv_lo, lc.b,
+                  lc.tb * TILE, lc.Lb);
+        if (t + 2 < hi) {
+          cursor_next<TT>(p, lc);
+          ld.issue(p, NT, total_chunks, cpr, row_lds, kv_lo, lc.b, lc.tb * TILE, lc.Lb);
+        }
+        lds_barrier();
+      }
     }
   }
-}
 
-// Per-launch dynamic LDS bytes for nkv KV heads per workgroup.
-inline size_t lds_bytes_for(int nkv, int D, int waves) {
-  const int row = nkv * (D + 8);
-  const int row_lds = row + ((row & 15) == 0 ? 8 : 0);
-  const size_t stage = ((size_t)TILE * row_lds + 15) & ~(size_t)15;
-  return 2 * stage + (size_t)waves * WSCR + 32 * sizeof(int);
+  // ---------------------------------------------------------------- arrivals and merges
+  if (npend == 0) return;
+  // Every wave waits for its own partial stores (agent-coherent) before the
+  // arrival is counted; the barrier then covers all waves of the workgroup.
+  vm_drain();
+  __syncthreads();
+  auto arrive = [&](int b, int Pb, int Tb) -> int {
+    const int pieces = range_owner(Pb + Tb - 1, T, Weff) - range_owner(Pb, T, Weff) + 1;
+    const int prev = __hip_atomic_fetch_add(p.counters + (int64_t)group * p.B + b, 1, __ATOMIC_RELAXED,
+                                            __HIP_MEMORY_SCOPE_AGENT);
+    return (prev == pieces - 1) ? 1 : 0;
+  };
+  if (tid == 0) {
+    misc[24] = arrive(pb0, pP0, pT0);
+    misc[25] = npend > 1 ? arrive(pb1, pP1, pT1) : 0;
+  }
+  __syncthreads();
+  // The last piece to arrive merges every piece of the sequence, in one pass
+  // with a running maximum (pieces are read agent-coherently, after the
+  // counter showed that all of them were published).
+  auto merge = [&](int b, int Pb, int Tb) {
+    const int w_first = range_owner(Pb, T, Weff);
+    const int w_last = range_owner(Pb + Tb - 1, T, Weff);
+    const int first_slot = (range_start(w_first, T, Weff) == Pb) ? 0 : 1;
+    // 4 consecutive dims per work item
+    for (int e = tid; e < (h1 - h0) * (D / 4); e += NT) {
+      const int h = h0 + e / (D / 4), d = (e - (e / (D / 4)) * (D / 4)) * 4;
+      float M = -INFINITY, Lsum = 0.f;
+      float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll 2
+      for (int w = w_first; w <= w_last; ++w) {
+        const int s = (w == w_first) ? first_slot : 0;
+        const int64_t base = ((int64_t)w * 2 + s) * p.H + h;
+        const float2 ml = load_pair_agent(p.part_ml + base * 2);
+        const float2 o01 = load_pair_agent(p.part_o + base * D + d);
+        const float2 o23 = load_pair_agent(p.part_o + base * D + d + 2);
+        const float Mn = fmaxf(M, ml.x);
+        const float a = __builtin_amdgcn_exp2f(M - Mn);        // 0 for the first piece (M = -inf)
+        const float sc = __builtin_amdgcn_exp2f(ml.x - Mn);
+        Lsum = Lsum * a + sc * ml.y;
+        O.x = O.x * a + sc * o01.x;
+        O.y = O.y * a + sc * o01.y;
+        O.z = O.z * a + sc * o23.x;
+        O.w = O.w * a + sc * o23.y;
+        M = Mn;
+      }
+      float r[4] = {O.x / Lsum, O.y / Lsum, O.z / Lsum, O.w / Lsum};
+      if constexpr (MODE == SRC_CHANNEL) {
+        if (p.use_quant) {
+          const int64_t kvg = h / G;
+#pragma unroll
+          for (int k = 0; k < 4; ++k) r[k] = h2f(p.vr0[kvg * D + d + k]) * (r[k] - h2f(p.vr1[kvg * D + d + k]));
+        }
+      }
+      const int64_t off = (int64_t)b * p.out_seq_stride + (int64_t)h * p.out_head_stride + d;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        if (p.out_f16) reinterpret_cast<uint16_t*>(p.out)[off + k] = f2h(r[k]);
+        else reinterpret_cast<float*>(p.out)[off + k] = r[k];
+      }
+    }
+    if (tid == 0)
+      __hip_atomic_store(p.counters + (int64_t)group * p.B + b, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  };
+  if (misc[24]) merge(pb0, pP0, pT0);
+  if (misc[25]) merge(pb1, pP1, pT1);
+  (void)VB;
 }
 
 }  // namespace attn
 
 // Launch one instantiation (defined in the per-mode translation units).
-int launch_attention_paged(int D, bool shared, bool fast, const AttnParams& p, dim3 grid, dim3 block,
+int launch_attention_paged(int D, bool shared, bool dma, const AttnParams& p, dim3 grid, dim3 block,
                            size_t lds, hipStream_t stream);
 int launch_attention_contig(int mode, int D, const AttnParams& p, dim3 grid, dim3 block, size_t lds,
                             hipStream_t stream);

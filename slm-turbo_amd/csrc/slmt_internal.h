@@ -42,6 +42,10 @@ enum : int {
 };
 
 template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u(uint32_t x) {
+  return __builtin_amdgcn_update_dpp(0u, x, CTRL, 0xf, 0xf, false);
+}
+template <int CTRL>
 __device__ __forceinline__ float dpp_f(float x) {
   return __builtin_bit_cast(
       float, __builtin_amdgcn_update_dpp(0u, __builtin_bit_cast(unsigned, x), CTRL, 0xf, 0xf, false));
@@ -162,15 +166,21 @@ struct AttnParams {
   int* counters;    // [groups][B]
   int W;            // workgroups per head group (grid.x)
   int min_tiles;    // minimum 16-token tiles per workgroup
+  int nthreads;     // threads per workgroup (blockDim.x)
 };
 
-// Geometry chosen on the host for a launch.
+// Geometry chosen on the host for a launch.  W_ws is the workgroup count the
+// workspace is sized for (the register-staged plan's, never below W).
 struct AttnPlan {
-  int heads_per_group, groups, waves, W;
+  int heads_per_group, groups, waves, W, W_ws;
+  bool dma;
   size_t lds_bytes;
 };
 
-int plan_attention(int B, int H, int G, int D, AttnPlan* plan);
+// dma_kv > 0 asks for the paged direct-load plan over a cache row of dma_kv
+// KV heads; it is taken when every head group covers whole, 16-byte aligned
+// KV heads and the LDS ring fits.
+int plan_attention(int B, int H, int G, int D, int dma_kv, AttnPlan* plan);
 int64_t attention_workspace_bytes(int B, int H, int KV, int D);
 int launch_attention(int mode, int D, AttnParams& p, void* workspace, int64_t ws_bytes,
                      hipStream_t stream);

@@ -46,7 +46,7 @@ SIGNATURES = {
 
 
 def library_path() -> Path:
-    return Path(os.environ.get("SLMT_LIB", str(LIB_PATH)))
+    return Path(os.environ.get("SLMT_LIB") or str(LIB_PATH))
 
 
 def load():
