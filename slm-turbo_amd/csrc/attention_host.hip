@@ -50,8 +50,12 @@ int plan_attention(int B, int H, int G, int D, int dma_kv, AttnPlan* plan) {
   size_t lds = attn::lds_geom(worst_nkv(hpg, G), D, waves).total;
   if (lds > 160 * 1024) return fail(SLMT_ERR_UNSUPPORTED, "attention: KV row too wide for LDS");
   int groups = (H + hpg - 1) / hpg;
-  auto workgroups = [&](size_t lds_b, int wv, int grp) {
-    int per_cu = 8 / wv;                            // up to 256 VGPRs per lane -> 8 waves per CU
+  // waves_cap: waves per CU the kernel's registers allow (the register-staged
+  // kernel may use up to 256 VGPRs: 2 waves per SIMD; the direct-load kernel
+  // stays within 168: 3 per SIMD).  The launch lowers W to the occupancy the
+  // runtime reports, so this is an upper bound for the workspace.
+  auto workgroups = [&](size_t lds_b, int wv, int grp, int waves_cap) {
+    int per_cu = waves_cap / wv;
     const int by_lds = (int)((160 * 1024) / lds_b);
     per_cu = per_cu < by_lds ? per_cu : by_lds;
     if (per_cu < 1) per_cu = 1;
@@ -61,7 +65,7 @@ int plan_attention(int B, int H, int G, int D, int dma_kv, AttnPlan* plan) {
   plan->heads_per_group = hpg;
   plan->groups = groups;
   plan->waves = waves;
-  plan->W = workgroups(lds, waves, groups);
+  plan->W = workgroups(lds, waves, groups, 8);
   plan->W_ws = plan->W;
   plan->dma = false;
   plan->lds_bytes = lds;
@@ -71,14 +75,14 @@ int plan_attention(int B, int H, int G, int D, int dma_kv, AttnPlan* plan) {
   // cache rows are a multiple of 16 bytes (an even number of KV heads), so a
   // wave's widened KV slot stays in its row.
   if (G % 4 != 0 || ((int64_t)dma_kv * (D + 8)) % 16 != 0) return SLMT_OK;
-  const int dh = hpg_max(H);
+  const int dh = hpg_max(H) < attn::DHEADS ? hpg_max(H) : attn::DHEADS;
   const int dwaves = dh / 4;
   const attn::DmaGeom geo = attn::dma_geom(D, dwaves);
   if (geo.total > 160 * 1024) return SLMT_OK;
   plan->heads_per_group = dh;
   plan->groups = (H + dh - 1) / dh;
   plan->waves = dwaves;
-  plan->W = workgroups((size_t)geo.total, dwaves, plan->groups);
+  plan->W = workgroups((size_t)geo.total, dwaves, plan->groups, 12);
   plan->dma = true;
   plan->lds_bytes = (size_t)geo.total;
   if (plan->W > plan->W_ws) plan->W_ws = plan->W;

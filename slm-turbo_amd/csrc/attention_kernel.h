@@ -58,15 +58,26 @@ constexpr int WSCR = 1024;         // per-wave LDS scratch bytes (query limbs / 
 constexpr int MAX_THREADS = 512;   // 8 waves: up to 256 VGPRs per wave
 constexpr int MAXP = 5;            // 8-byte chunks prefetched per thread (general path)
 constexpr int DSTAGE = 3;          // LDS ring depth of the direct-load path
+constexpr int DHEADS = 32;         // query heads (4 per wave) per workgroup, direct-load path
 constexpr int QSLOT = 1024;        // LDS bytes of one wave's query rows in a ring slot
 
 __device__ __forceinline__ float readlane_f(float x, int l) {
   return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), l));
 }
 __device__ __forceinline__ int uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
+// Lane i's 32-bit word, zero-extended when widened (the builtin returns a
+// signed int, which would sign-extend the low word of an address).
+__device__ __forceinline__ uint32_t readlane_u32(uint32_t x, int i) {
+  return (uint32_t)__builtin_amdgcn_readlane((int)x, i);
+}
 
 __device__ __forceinline__ float fdot2(uint32_t a, uint32_t b, float c) {
   return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, a), __builtin_bit_cast(f16x2, b), c, false);
+}
+
+// Two bytes at bits 0-7 and 16-23 (zero elsewhere): one v_perm_b32.
+__device__ __forceinline__ uint32_t pack_pair(uint32_t b0, uint32_t b1) {
+  return __builtin_amdgcn_perm(b1, b0, 0x0C040C00u);
 }
 
 // Workgroup barrier that orders LDS only: global loads issued before it stay
@@ -97,8 +108,9 @@ __device__ __forceinline__ void vm_wait_n() {
 // only make the wait stricter.
 template <int OPS>
 __device__ __forceinline__ void vm_wait_tiles(int ahead) {   // ahead wave-uniform, 0 .. DSTAGE-2
-  static_assert(DSTAGE == 3, "one case per possible look-ahead");
-  if (ahead >= 1) vm_wait_n<OPS>();
+  static_assert(DSTAGE >= 2 && DSTAGE <= 4, "one case per possible look-ahead");
+  if (DSTAGE > 3 && ahead >= 2) vm_wait_n<2 * OPS>();
+  else if (DSTAGE > 2 && ahead >= 1) vm_wait_n<OPS>();
   else vm_wait_n<0>();
 }
 
@@ -546,7 +558,7 @@ struct Heads {
       const uint4 wq = *reinterpret_cast<const uint4*>(wscr + pr2 * 16);
       if constexpr (SHARED) {
         const uint8_t* vb = S + kvw[0] * SLOT + VB + jj;
-        const uint32_t tw = (uint32_t)vb[(2 * pr2) * row_lds] | ((uint32_t)vb[(2 * pr2 + 1) * row_lds] << 16);
+        const uint32_t tw = pack_pair(vb[(2 * pr2) * row_lds], vb[(2 * pr2 + 1) * row_lds]);
         const uint32_t vlo = tw & 0x000F000Fu;
         acc[0][0] = fdot2(wq.x, vlo, acc[0][0]);
         acc[0][1] = fdot2(wq.x, tw, acc[0][1]);
@@ -561,7 +573,7 @@ struct Heads {
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           const uint8_t* vb = S + kvw[g] * SLOT + VB + jj;
-          const uint32_t tw = (uint32_t)vb[(2 * pr2) * row_lds] | ((uint32_t)vb[(2 * pr2 + 1) * row_lds] << 16);
+          const uint32_t tw = pack_pair(vb[(2 * pr2) * row_lds], vb[(2 * pr2 + 1) * row_lds]);
           acc[g][0] = fdot2(wgs[g], tw & 0x000F000Fu, acc[g][0]);
           acc[g][1] = fdot2(wgs[g], tw, acc[g][1]);
         }
@@ -772,7 +784,8 @@ __global__ void __launch_bounds__(MAX_THREADS) attention_kernel(const AttnParams
         if (!hd.hw[g] || !wr) continue;
         const int h = h0 + wave * 4 + g;
         const float L = readlane_f(lt, g);
-        float r0 = o[g][0] / L, r1 = o[g][1] / L;
+        const float rL = __builtin_amdgcn_rcpf(L);
+        float r0 = o[g][0] * rL, r1 = o[g][1] * rL;
         if constexpr (MODE == SRC_CHANNEL) {
           if (p.use_quant) {
             const int64_t kvg = h / G;
@@ -854,56 +867,83 @@ __global__ void __launch_bounds__(MAX_THREADS) attention_kernel(const AttnParams
     // Every wave runs its own ring of DSTAGE slots (no workgroup barriers):
     // tiles lo .. lo+DSTAGE-2 are issued up front; iteration t waits for tile
     // t, issues tile t+DSTAGE-1 into the slot tile t-1 used, computes tile t.
-    // The block-table entries of the next tile to issue are loaded one
-    // iteration early and kept raw until used, so their loads are not waited
-    // on where they are issued.  Entries are read as their low 32 bits
-    // (physical blocks are below 2^31: the host checks num_blocks), so 32-
-    // and 64-bit tables take the same path.
+    //
+    // Tile descriptors are built 64 tiles at a time, lane i for tile
+    // dchunk + i: the slot bases of rows 0-15 and 16-31 and the sequence
+    // whose query rows ride with the tile (-1 if none).  An issue then reads
+    // them with v_readlane instead of walking the block table in scalar code.
+    // Block-table entries are read as their low 32 bits (physical blocks are
+    // below 2^31: the host checks num_blocks), so 32- and 64-bit tables share
+    // the path.
     const int esh = p.bt64 ? 3 : 2;
     const uint8_t* btab = reinterpret_cast<const uint8_t*>(p.block_tables);
-    auto entry_of = [&](int b, int tok) -> int32_t {
-      return sload_i32(btab + (((int64_t)b * p.bt_stride + (tok >> p.block_shift)) << esh), 0);
+    uint32_t d0lo = 0, d0hi = 0, d1lo = 0, d1hi = 0;
+    int dq = -1;
+    int dchunk = lo;
+    // c: cursor at tile `first` (global index)
+    auto build = [&](const Cursor& c, int first) {
+      const int t = first + lane;
+      int b = c.b, P = c.Pb, Tb = c.Tb, L = c.Lb;
+      int mb = -1, mtb = 0, mL = 0;
+      for (;;) {
+        if (t >= P && t < P + Tb) {
+          mb = b;
+          mtb = t - P;
+          mL = L;
+        }
+        P += Tb;
+        if (!__builtin_amdgcn_ballot_w64(t >= P && t < hi) || b + 1 >= p.B) break;
+        ++b;
+        L = b == c.b + 1 ? c.Lnext : seq_len_of(p, b);
+        Tb = tiles_of<TT>(L);
+      }
+      uint64_t base0 = reinterpret_cast<uint64_t>(p.cache), base1 = base0;
+      dq = -1;
+      if (mb >= 0 && t < hi) {
+        const int tok0 = mtb * DTILE;
+        const bool upper = tok0 + 16 < mL;
+        const int64_t row_e = (int64_t)mb * p.bt_stride;
+        const int32_t e0 = *reinterpret_cast<const int32_t*>(btab + ((row_e + (tok0 >> p.block_shift)) << esh));
+        const int32_t e1 =
+            upper ? *reinterpret_cast<const int32_t*>(btab + ((row_e + ((tok0 + 16) >> p.block_shift)) << esh)) : e0;
+        base0 += (uint64_t)(uint32_t)e0 * (uint64_t)blk_bytes + (uint64_t)((tok0 & (p.block_size - 1)) * cache_row);
+        base1 = upper ? reinterpret_cast<uint64_t>(p.cache) + (uint64_t)(uint32_t)e1 * (uint64_t)blk_bytes +
+                            (uint64_t)(((tok0 + 16) & (p.block_size - 1)) * cache_row)
+                      : base0;
+        dq = (mtb == 0 || t == lo) ? mb : -1;
+      }
+      d0lo = (uint32_t)base0;
+      d0hi = (uint32_t)(base0 >> 32);
+      d1lo = (uint32_t)base1;
+      d1hi = (uint32_t)(base1 >> 32);
+      dchunk = first;
     };
-    // slot base of token tok of a tile (rows of the same block follow)
-    auto slot_base = [&](int32_t phys, int tok) -> const uint8_t* {
-      return p.cache + (int64_t)phys * blk_bytes + (int64_t)(tok & (p.block_size - 1)) * cache_row;
+    auto issue_desc = [&](int t, int st) {
+      const int i = t - dchunk;
+      const uint64_t b0 = (uint64_t)readlane_u32(d0lo, i) | ((uint64_t)readlane_u32(d0hi, i) << 32);
+      const uint64_t b1 = (uint64_t)readlane_u32(d1lo, i) | ((uint64_t)readlane_u32(d1hi, i) << 32);
+      dma_tile(reinterpret_cast<const uint8_t*>(b0), reinterpret_cast<const uint8_t*>(b1), st,
+               __builtin_amdgcn_readlane(dq, i));
     };
-    Cursor dc = cc;
-    int32_t pf0 = 0, pf1 = 0;  // entries of the tile after dc (rows 0-15, 16-31) when pf_ok
-    bool pf_ok = false;
-    auto prefetch_after = [&](const Cursor& c) {
-      // tile following c: same sequence, or the first tile of sequence b+1
-      // when that one is not empty (else looked up at issue); the loads
-      // always go to valid entries so that nothing branches around them
-      const bool same = c.tb + 1 < c.Tb;
-      const bool next_ok = c.Lnext > 0 && c.b + 1 < p.B;
-      pf_ok = same || next_ok;
-      const int nb = same ? c.b : (next_ok ? c.b + 1 : c.b);
-      const int ntok = same ? (c.tb + 1) * DTILE : (next_ok ? 0 : c.tb * DTILE);
-      const int nL = same ? c.Lb : (next_ok ? c.Lnext : c.Lb);
-      pf0 = entry_of(nb, ntok);
-      pf1 = entry_of(nb, ntok + 16 < nL ? ntok + 16 : ntok);
-    };
-    auto issue = [&](const Cursor& c, bool use_pf, int st, int qb) {
-      const int tok0 = c.tb * DTILE;
-      const bool upper = tok0 + 16 < c.Lb;     // rows 16-31 hold tokens of the sequence
-      const int32_t e0 = use_pf ? pf0 : entry_of(c.b, tok0);
-      const int32_t e1 = use_pf ? pf1 : entry_of(c.b, upper ? tok0 + 16 : tok0);
-      const uint8_t* b0 = slot_base(e0, tok0);
-      dma_tile(b0, upper ? slot_base(e1, tok0 + 16) : b0, st, qb);
-    };
+    Cursor dc = cc;                                 // cursor of the next tile to issue
+    build(dc, lo);
     for (int j = 0; j < DSTAGE - 1 && lo + j < hi; ++j) {
-      if (j > 0) cursor_next<TT>(p, dc);
-      issue(dc, false, (lo + j) % DSTAGE, (j == 0 || dc.tb == 0) ? dc.b : -1);
+      issue_desc(lo + j, (lo + j) % DSTAGE);
+      cursor_next<TT>(p, dc);
     }
-    prefetch_after(dc);
     int st = lo % DSTAGE;                           // ring slot of tile t
     for (int t = lo; t < hi; ++t) {
+      // alternate the two waves of a SIMD (waves w and w+4) in priority
+      if (((t - lo) & 7) == 0) {
+        if ((((t - lo) >> 3) + (wave >> 2)) & 1) __builtin_amdgcn_s_setprio(1);
+        else __builtin_amdgcn_s_setprio(0);
+      }
       vm_wait_tiles<ISSUES>(min(DSTAGE - 2, hi - 1 - t));
-      if (t + DSTAGE - 1 < hi) {
+      const int tn = t + DSTAGE - 1;
+      if (tn < hi) {
+        if (tn - dchunk >= 64) build(dc, tn);
+        issue_desc(tn, st == 0 ? DSTAGE - 1 : st - 1);
         cursor_next<TT>(p, dc);
-        issue(dc, pf_ok, st == 0 ? DSTAGE - 1 : st - 1, dc.tb == 0 ? dc.b : -1);
-        prefetch_after(dc);
       }
       const bool seg_start = (t == lo) || (cc.tb == 0);
       const bool seg_end = (t == hi - 1) || (cc.tb == cc.Tb - 1);
@@ -916,6 +956,7 @@ __global__ void __launch_bounds__(MAX_THREADS) attention_kernel(const AttnParams
       if (t + 1 < hi) cursor_next<TT>(p, cc);
       st = st + 1 == DSTAGE ? 0 : st + 1;
     }
+    __builtin_amdgcn_s_setprio(0);
   } else {
     // ---------------------------------------------------------------- register-staged pipeline
     Cursor lc = cc;                          // loader cursor runs one tile ahead
@@ -996,7 +1037,8 @@ __global__ void __launch_bounds__(MAX_THREADS) attention_kernel(const AttnParams
         O.w = O.w * a + sc * o23.y;
         M = Mn;
       }
-      float r[4] = {O.x / Lsum, O.y / Lsum, O.z / Lsum, O.w / Lsum};
+      const float rL = __builtin_amdgcn_rcpf(Lsum);
+      float r[4] = {O.x * rL, O.y * rL, O.z * rL, O.w * rL};
       if constexpr (MODE == SRC_CHANNEL) {
         if (p.use_quant) {
           const int64_t kvg = h / G;
