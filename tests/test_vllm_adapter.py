@@ -1,0 +1,225 @@
+"""vLLM backend surface (reference adapters/vllm_adapter.py:102-336) without vLLM.
+
+CPU tests drive the backend with a fake ``attn_metadata`` (the fields the
+reference reads: seq_lens, block_table, num_actual_tokens, max_query_len)
+and a recording stand-in for the kernel module, to check the static surface,
+degraded mode and the dispatch (one batched decode launch per layer, the
+store's arguments, prefill routing).  GPU tests run the real kernels through
+the backend against the oracle.
+"""
+from types import SimpleNamespace
+
+import numpy as np
+import pytest
+import torch
+
+from adapters import vllm_adapter as va
+from common import assert_close, make_paged_case, paged_reference
+from oracle import quant as oq
+
+
+class _RecordingKernels:
+    """Stand-in for kernels.kv_dequant that records calls."""
+
+    def __init__(self):
+        self.decode_calls = []
+        self.store_calls = []
+
+    def kv_dequant_decode_paged_batched(self, q, kv_cache, block_tables, seq_lens, block_size, num_kv_heads,
+                                        out=None, out_dtype=None):
+        self.decode_calls.append(dict(q=q, kv_cache=kv_cache, block_tables=block_tables, seq_lens=seq_lens,
+                                      block_size=block_size, num_kv_heads=num_kv_heads, out=out))
+        res = torch.full(q.shape, 0.5, dtype=out.dtype if out is not None else (out_dtype or torch.float32))
+        if out is not None:
+            out.copy_(res)
+            return out
+        return res
+
+    def kv_quantize_store(self, key, value, kv_cache, slot_mapping, block_size):
+        self.store_calls.append(dict(key=key, value=value, kv_cache=kv_cache, slot_mapping=slot_mapping,
+                                     block_size=block_size))
+
+
+def _impl(H=8, D=64, KV=2, kernels=None):
+    impl = va.QuantizedKVAttentionImpl(num_heads=H, head_size=D, scale=D ** -0.5, num_kv_heads=KV)
+    if kernels is not None:
+        impl._slm_ops = kernels
+    return impl
+
+
+def _meta(seq_lens, block_table, max_query_len=1, n=None):
+    seq_lens = torch.as_tensor(seq_lens, dtype=torch.int32)
+    return SimpleNamespace(seq_lens=seq_lens, block_table=torch.as_tensor(block_table, dtype=torch.int32),
+                           num_actual_tokens=len(seq_lens) if n is None else n, max_query_len=max_query_len)
+
+
+# ---------------------------------------------------------------- static surface
+def test_backend_static_surface():
+    B = va.QuantizedKVAttentionBackend
+    assert B.get_name() == "CUSTOM"
+    assert B.get_impl_cls() is va.QuantizedKVAttentionImpl
+    assert B.get_kv_cache_shape(100, 16, 8, 128) == (100, 16, 8, 136)
+    assert B.get_kv_cache_shape(7, 32, 2, 64, "auto") == (7, 32, 2, 72)
+    assert B.supports_batch_invariance() is True
+    with pytest.raises(NotImplementedError):
+        B.get_kv_cache_stride_order()
+    assert va.packed_slot_bytes(80) == 88
+    assert va.SUPPORTED_HEAD_SIZES == (64, 80, 128)
+
+
+def test_degraded_mode_without_vllm():
+    assert not va.VLLM_AVAILABLE and va.VLLM_IMPORT_ERROR
+    assert va.register_plugin() is None        # no vLLM: nothing registered, no exception
+    assert va.register_plugin() is None        # idempotent
+    assert va._register_custom_backend() is False
+    assert va._patch_attention_layer_spec() is False
+    st = va.backend_status()
+    assert st["vllm_available"] is False and st["backend_registered"] is False
+    assert {"kernels", "kernel_calls"} <= set(st)
+
+
+def test_impl_needs_the_kernel_library(monkeypatch):
+    from kernels import _native
+
+    def broken():
+        raise RuntimeError("slm-turbo HIP library not found at /nowhere")
+    monkeypatch.setattr(_native, "load", broken)
+    impl = _impl()
+    with pytest.raises(RuntimeError, match="library not found"):
+        impl.do_kv_cache_update(None, torch.zeros(1, 2, 64), torch.zeros(1, 2, 64),
+                                torch.zeros(1, 16, 2, 72, dtype=torch.uint8), torch.zeros(1, dtype=torch.int64))
+
+
+# ---------------------------------------------------------------- dispatch
+def test_decode_is_one_batched_launch_per_layer():
+    k = _RecordingKernels()
+    impl = _impl(H=8, D=64, KV=2, kernels=k)
+    N = 5
+    q = torch.randn(N, 8, 64).half()
+    cache = torch.zeros(9, 16, 2, 72, dtype=torch.uint8)
+    tables = torch.arange(N * 3, dtype=torch.int32).reshape(N, 3) % 9
+    meta = _meta([3, 40, 0, 17, 33], tables)
+    out = torch.zeros(N, 8 * 64, dtype=torch.float16)
+    res = impl.forward(None, q, q, q, cache, meta, out)
+    assert res is out
+    assert len(k.decode_calls) == 1                 # not one per request
+    c = k.decode_calls[0]
+    assert c["q"].shape == (N, 8, 64) and c["block_size"] == 16 and c["num_kv_heads"] == 2
+    assert c["seq_lens"].dtype == torch.int32 and torch.equal(c["seq_lens"], meta.seq_lens)
+    assert c["block_tables"].dtype == torch.int32   # vLLM's int32 table, not copied to int64
+    assert torch.equal(c["block_tables"], tables)
+    assert c["out"] is not None and c["out"].data_ptr() == out.data_ptr()   # written in place
+    assert torch.all(out == 0.5)
+
+
+def test_decode_only_the_actual_tokens():
+    k = _RecordingKernels()
+    impl = _impl(kernels=k)
+    q = torch.randn(6, 8, 64).half()
+    meta = _meta([5, 6, 7, 8], torch.zeros(4, 2, dtype=torch.int32), n=3)
+    out = torch.full((6, 512), -1.0, dtype=torch.float16)
+    impl.forward(None, q, q, q, torch.zeros(2, 16, 2, 72, dtype=torch.uint8), meta, out)
+    c = k.decode_calls[0]
+    assert c["q"].shape[0] == 3 and c["seq_lens"].numel() == 3 and c["block_tables"].shape[0] == 3
+    assert torch.all(out[:3] == 0.5) and torch.all(out[3:] == -1.0)
+
+
+def test_decode_into_non_contiguous_output_copies():
+    k = _RecordingKernels()
+    impl = _impl(kernels=k)
+    q = torch.randn(2, 8, 64).half()
+    big = torch.zeros(2, 1024, dtype=torch.float16)
+    out = big[:, :512]                                  # non-contiguous view
+    impl.forward(None, q, q, q, torch.zeros(2, 16, 2, 72, dtype=torch.uint8),
+                 _meta([4, 4], torch.zeros(2, 1, dtype=torch.int32)), out)
+    assert k.decode_calls[0]["out"] is None
+    assert torch.all(big[:, :512] == 0.5) and torch.all(big[:, 512:] == 0)
+
+
+def test_empty_or_missing_metadata_gives_zeros():
+    k = _RecordingKernels()
+    impl = _impl(kernels=k)
+    q = torch.randn(3, 8, 64).half()
+    cache = torch.zeros(2, 16, 2, 72, dtype=torch.uint8)
+    out = torch.ones(3, 512, dtype=torch.float16)
+    assert torch.all(impl.forward(None, q, q, q, cache, None, out) == 0)
+    out.fill_(1)
+    meta = _meta([1, 1, 1], torch.zeros(3, 1, dtype=torch.int32), n=0)
+    assert torch.all(impl.forward(None, q, q, q, cache, meta, out) == 0)
+    assert torch.all(impl.forward(None, q, q, q, cache, meta, None) == 0)   # allocates the output
+    assert not k.decode_calls
+
+
+def test_store_arguments():
+    k = _RecordingKernels()
+    impl = _impl(kernels=k)
+    key = torch.randn(4, 2, 64).half()
+    cache = torch.zeros(3, 32, 2, 72, dtype=torch.uint8)
+    slots = torch.tensor([0, 5, -1, 70])
+    impl.do_kv_cache_update(None, key, key, cache, slots)
+    assert len(k.store_calls) == 1 and k.store_calls[0]["block_size"] == 32
+    assert k.store_calls[0]["slot_mapping"] is slots
+    impl.do_kv_cache_update(None, key, key, torch.zeros(0, 32, 2, 72, dtype=torch.uint8), slots)
+    impl.do_kv_cache_update(None, key, key, None, slots)
+    assert len(k.store_calls) == 1                     # empty / missing cache: nothing stored
+
+
+def test_prefill_routes_to_causal_sdpa_over_the_chunk():
+    """max_query_len > 1: causal attention over the chunk's raw K/V with the
+    layer's scale and GQA (reference :231-245); checked on the CPU against
+    an explicit float64 causal softmax."""
+    k = _RecordingKernels()
+    H, KV, D, N = 8, 2, 64, 6
+    impl = _impl(H=H, D=D, KV=KV, kernels=k)
+    g = torch.Generator().manual_seed(3)
+    q = torch.randn(N, H, D, generator=g)
+    key = torch.randn(N, KV, D, generator=g)
+    val = torch.randn(N, KV, D, generator=g)
+    out = torch.zeros(N, H * D)
+    impl.forward(None, q, key, val, torch.zeros(1, 16, KV, D + 8, dtype=torch.uint8),
+                 _meta([N], torch.zeros(1, 1), max_query_len=N, n=N), out)
+    assert not k.decode_calls
+    qd, kd, vd = q.double(), key.double(), val.double()
+    ref = torch.zeros(N, H, D, dtype=torch.float64)
+    for h in range(H):
+        kv = h // (H // KV)
+        s = (qd[:, h] @ kd[:, kv].T) * D ** -0.5
+        s = s.masked_fill(torch.triu(torch.ones(N, N, dtype=torch.bool), 1), float("-inf"))
+        ref[:, h] = torch.softmax(s, -1) @ vd[:, kv]
+    assert_close(out.reshape(N, H, D).numpy(), ref.numpy(), atol=1e-5, rtol=1e-5)
+
+
+# ---------------------------------------------------------------- on the GPU
+@pytest.mark.gpu
+def test_backend_decode_matches_oracle_with_vllm_metadata():
+    """Real kernels through the backend: int32 block table and int32 device
+    seq_lens as vLLM passes them, fp16 output written in place."""
+    H, KV, D = 32, 8, 128
+    case = make_paged_case(seed=77, B=6, H=H, KV=KV, D=D, lens=[1, 900, 0, 2500, 33, 4096])
+    ref = paged_reference(case)
+    impl = _impl(H=H, D=D, KV=KV)
+    dev = "cuda:0"
+    q = case.q.to(dev)
+    cache = torch.from_numpy(case.kv_cache).to(dev)
+    meta = _meta(case.seq_lens, case.block_tables)
+    meta.seq_lens, meta.block_table = meta.seq_lens.to(dev), meta.block_table.to(dev)
+    out = torch.zeros(6, H * D, dtype=torch.float16, device=dev)
+    impl.forward(None, q, q, q, cache, meta, out)
+    torch.cuda.synchronize()
+    assert_close(out.float().cpu().numpy().reshape(6, H, D), ref, atol=3e-3, what="backend decode")
+
+
+@pytest.mark.gpu
+def test_backend_store_is_bit_exact():
+    H, KV, D, bs = 8, 2, 80, 16
+    g = torch.Generator().manual_seed(5)
+    key = torch.randn(11, KV, D, generator=g).half()
+    val = torch.randn(11, KV, D, generator=g).half()
+    slots = torch.tensor([3, 4, 5, -1, 17, 18, 40, 41, 63, 0, 1], dtype=torch.int64)
+    ref = np.zeros((4, bs, KV, D + 8), dtype=np.uint8)
+    oq.quantize_store(key.numpy(), val.numpy(), ref, slots.numpy(), bs)
+    impl = _impl(H=H, D=D, KV=KV)
+    cache = torch.zeros(ref.shape, dtype=torch.uint8, device="cuda:0")
+    impl.do_kv_cache_update(None, key.cuda(), val.cuda(), cache, slots.cuda())
+    torch.cuda.synchronize()
+    assert np.array_equal(cache.cpu().numpy(), ref)
