@@ -118,7 +118,8 @@ def cpu_baseline(lens, tables, q, cache_gpu, out_gpu, budget_s: float):
 
     from oracle import cpu_path
 
-    cores = len(os.sched_getaffinity(0))
+    # the host's share for one GPU: OMP_NUM_THREADS when set, never more than the affinity mask
+    cores = min(len(os.sched_getaffinity(0)), int(os.environ.get("OMP_NUM_THREADS") or 16))
     torch.set_num_threads(cores)
     cache = cache_gpu.cpu()
     qc = q.cpu()
@@ -182,7 +183,7 @@ def main(argv=None) -> int:
     lib = _native.load()
     ws, ws_bytes = kd._workspace(lib, dev, B, H, KV, D)
     stream = torch.cuda.current_stream(dev)
-    fn = lib.slmt_decode_paged
+    fn = lib.slmt_decode_paged_batched
     argsets = [(q.data_ptr(), H * D, D, c.data_ptr(), nb, BS, tables_d.data_ptr(), 32, tables_d.stride(0),
                 lens_d.data_ptr(), 0, B, H, KV, D, out.data_ptr(), _native.OUT_F32, H * D, D, ws, ws_bytes,
                 stream.cuda_stream) for q, c in zip(qs, caches)]

@@ -45,7 +45,7 @@ enum { SLMT_OUT_F32 = 0, SLMT_OUT_F16 = 1 };
 const char* slmt_last_error(void);
 
 /* ABI version of this library (SLMT_ABI_VERSION). */
-#define SLMT_ABI_VERSION 1
+#define SLMT_ABI_VERSION 2
 int slmt_abi_version(void);
 
 /* Bytes of caller-owned workspace the attention entry points need.  A
@@ -105,14 +105,32 @@ int slmt_quantize_per_channel(const void* x, int num_kv_heads, int seq_len, int 
  * length 0 produce zeros.
  * workspace: slmt_attention_workspace_bytes(B, num_heads, num_kv_heads, D).
  */
-int slmt_decode_paged(const void* q, int64_t q_seq_stride, int64_t q_head_stride,
-                      const void* kv_cache, int64_t num_blocks, int block_size,
-                      const void* block_tables, int block_table_bits,
-                      int64_t block_table_stride,
-                      const int32_t* seq_lens, int fixed_seq_len,
-                      int num_seqs, int num_heads, int num_kv_heads, int head_dim,
-                      void* out, int out_dtype, int64_t out_seq_stride, int64_t out_head_stride,
-                      void* workspace, int64_t workspace_bytes, slmt_stream_t stream);
+int slmt_decode_paged_batched(const void* q, int64_t q_seq_stride, int64_t q_head_stride,
+                              const void* kv_cache, int64_t num_blocks, int block_size,
+                              const void* block_tables, int block_table_bits,
+                              int64_t block_table_stride,
+                              const int32_t* seq_lens, int fixed_seq_len,
+                              int num_seqs, int num_heads, int num_kv_heads, int head_dim,
+                              void* out, int out_dtype, int64_t out_seq_stride,
+                              int64_t out_head_stride, void* workspace, int64_t workspace_bytes,
+                              slmt_stream_t stream);
+
+/*
+ * Paged decode of ONE request.  Replaces
+ * kv_dequant_decode_per_token_paged_attention_cuda (reference
+ * kernels/kv_dequant_cuda.cu:355-410), bound from kernels/kv_dequant.py:236-257.
+ *   q:           fp16 [H, 1, D] contiguous
+ *   kv_cache:    uint8 [num_blocks, block_size, KV, D+8]
+ *   block_table: int64 [>= ceil(seq_len/block_size)] on the device
+ *   out:         fp32 [H, 1, D]
+ * seq_len 0 writes zeros (the Python binding returns NaN like the reference's
+ * 0/0 softmax).  A batch of one through slmt_decode_paged_batched.
+ * workspace: slmt_attention_workspace_bytes(1, num_heads, num_kv_heads, D).
+ */
+int slmt_decode_paged(const void* q, const void* kv_cache, int64_t num_blocks, int block_size,
+                      const int64_t* block_table, int seq_len, int num_heads, int num_kv_heads,
+                      int head_dim, float* out, void* workspace, int64_t workspace_bytes,
+                      slmt_stream_t stream);
 
 /*
  * Per-token decode over contiguous buffers.  Replaces

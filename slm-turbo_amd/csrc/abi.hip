@@ -140,12 +140,13 @@ int slmt_quantize_per_channel(const void* x, int num_kv_heads, int seq_len, int 
                                      reinterpret_cast<hipStream_t>(stream));
 }
 
-int slmt_decode_paged(const void* q, int64_t q_seq_stride, int64_t q_head_stride, const void* kv_cache,
-                      int64_t num_blocks, int block_size, const void* block_tables, int block_table_bits,
-                      int64_t block_table_stride, const int32_t* seq_lens, int fixed_seq_len,
-                      int num_seqs, int num_heads, int num_kv_heads, int head_dim, void* out,
-                      int out_dtype, int64_t out_seq_stride, int64_t out_head_stride, void* workspace,
-                      int64_t workspace_bytes, slmt_stream_t stream) {
+int slmt_decode_paged_batched(const void* q, int64_t q_seq_stride, int64_t q_head_stride,
+                              const void* kv_cache, int64_t num_blocks, int block_size,
+                              const void* block_tables, int block_table_bits, int64_t block_table_stride,
+                              const int32_t* seq_lens, int fixed_seq_len, int num_seqs, int num_heads,
+                              int num_kv_heads, int head_dim, void* out, int out_dtype,
+                              int64_t out_seq_stride, int64_t out_head_stride, void* workspace,
+                              int64_t workspace_bytes, slmt_stream_t stream) {
   clear_error();
   const char* ph = "paged decode";
   if (!head_dim_ok(head_dim)) return fail(SLMT_ERR_INVALID, "paged decode: head_dim must be 64/80/128, got " + s(head_dim));
@@ -189,6 +190,22 @@ int slmt_decode_paged(const void* q, int64_t q_seq_stride, int64_t q_head_stride
   p.out_seq_stride = out_seq_stride;
   p.out_head_stride = out_head_stride;
   return launch_attention(SRC_PAGED, head_dim, p, workspace, workspace_bytes, reinterpret_cast<hipStream_t>(stream));
+}
+
+int slmt_decode_paged(const void* q, const void* kv_cache, int64_t num_blocks, int block_size,
+                      const int64_t* block_table, int seq_len, int num_heads, int num_kv_heads,
+                      int head_dim, float* out, void* workspace, int64_t workspace_bytes,
+                      slmt_stream_t stream) {
+  // One request = a batch of one with a fixed length and an int64 block row.
+  if (seq_len < 0) {
+    clear_error();
+    return fail(SLMT_ERR_INVALID, "paged decode: seq_len must be >= 0");
+  }
+  return slmt_decode_paged_batched(q, (int64_t)num_heads * head_dim, head_dim, kv_cache, num_blocks,
+                                   block_size, block_table, 64, 0, nullptr, seq_len, 1, num_heads,
+                                   num_kv_heads, head_dim, out, SLMT_OUT_F32,
+                                   (int64_t)num_heads * head_dim, head_dim, workspace, workspace_bytes,
+                                   stream);
 }
 
 int slmt_decode_per_token(const void* q, const void* k_packed, const void* k_min, const void* k_step,

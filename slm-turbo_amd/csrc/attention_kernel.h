@@ -9,23 +9,26 @@
 //               (kernels/kv_dequant_kernels.cuh:113-275, 293-502)
 //
 // Design (GEMV-shaped and bandwidth-bound; no MFMA):
-// * Work split: the tokens of all sequences are cut into 16-token tiles; the
-//   concatenated tile list is divided evenly over W workgroups ("stream-K").
-//   A workgroup walks its tile range, which may cover the end of one
-//   sequence, whole sequences and the start of another.  A sequence split
-//   over several workgroups is merged by the last workgroup to finish its
-//   piece (log-sum-exp merge of (m, l, o) partials; arrival counter per
-//   sequence), so one launch produces the final output.  Arrivals are
-//   counted once the workgroup has finished its whole range, so the load
-//   pipeline never drains in the middle of it.
-// * Staging, paged fast path: a tile (16 tokens x every KV head) is one
-//   contiguous byte range of the cache.  It is copied straight into LDS with
-//   16-byte direct loads (global_load_lds_dwordx4, no VGPRs) into a ring of
-//   NSTAGE buffers, so NSTAGE-1 tiles are in flight while one is computed.
-//   Each wave waits for its own direct loads with an exact vmcnt and a
-//   workgroup barrier publishes the tile.  The query of a sequence rides in
-//   the same ring (one more direct load per wave), block-table entries and
-//   lengths are scalar loads fetched a tile ahead.
+// * Work split: the tokens of all sequences are cut into tiles (32 tokens on
+//   the direct-load path, 16 otherwise); the concatenated tile list is
+//   divided evenly over W workgroups ("stream-K").  A workgroup walks its
+//   tile range, which may cover the end of one sequence, whole sequences and
+//   the start of another.  A sequence split over several workgroups is
+//   merged by the last workgroup to finish its piece (log-sum-exp merge of
+//   (m, l, o) partials; arrival counter per sequence), so one launch
+//   produces the final output.  Arrivals are counted once the workgroup has
+//   finished its whole range, so the load pipeline never drains in the
+//   middle of it.
+// * Staging, paged fast path (power-of-two block >= 16 tokens, 4 query heads
+//   per KV head): each wave owns one KV head and a private LDS ring of
+//   DSTAGE stages.  A 32-token tile of that head is two runs of 16
+//   consecutive slots; the wave copies the K/V bytes and rulers of those
+//   slots straight into its ring with 16-byte direct loads
+//   (global_load_lds_dwordx4, no VGPRs), DSTAGE-1 tiles ahead, and waits for
+//   them with an exact vmcnt -- no workgroup barrier anywhere in the loop.
+//   The query rows of a new sequence ride in the same ring.  Block-table
+//   entries for 64 tiles at a time are gathered into per-lane descriptors
+//   and read back with readlane, so the loop issues no table loads.
 // * Staging, general path (other layouts): the next tile's 8-byte chunks are
 //   held in registers while the current one is computed, double-buffered.
 // * QK (lane = token p x query head g of the wave's 4 heads): the query is

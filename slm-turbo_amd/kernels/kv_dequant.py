@@ -323,12 +323,11 @@ def kv_dequant_decode_per_token_paged_attention(
                  f"paged decode: block_table holds {block_table.numel()} blocks, fewer than seq_len {seq_len} needs")
         q = q.contiguous()
         kv_cache = kv_cache.contiguous()
-        block_table = block_table.contiguous()
+        block_table = block_table.to(device=dev, dtype=torch.int64).contiguous()
         ws, ws_bytes = _workspace(lib, dev, 1, H, num_kv_heads, D)
         rc = lib.slmt_decode_paged(
-            _ptr(q), H * D, D, _ptr(kv_cache), kv_cache.size(0), int(block_size), _ptr(block_table),
-            64 if block_table.dtype == torch.int64 else 32, 0, None, seq_len, 1, H, num_kv_heads, D,
-            _ptr(out), _native.OUT_F32, H * D, D, ws, ws_bytes, _stream(dev))
+            _ptr(q), _ptr(kv_cache), kv_cache.size(0), int(block_size), _ptr(block_table), seq_len,
+            H, num_kv_heads, D, _ptr(out), ws, ws_bytes, _stream(dev))
         _native.check(lib, rc)
     return out
 
@@ -380,7 +379,7 @@ def kv_dequant_decode_paged_batched(
             q = q.contiguous()
         seq_lens = seq_lens.contiguous()
         ws, ws_bytes = _workspace(lib, dev, B, H, num_kv_heads, D)
-        rc = lib.slmt_decode_paged(
+        rc = lib.slmt_decode_paged_batched(
             _ptr(q), q.stride(0), q.stride(1), _ptr(kv_cache), kv_cache.size(0), int(block_size),
             _ptr(block_tables), 64 if block_tables.dtype == torch.int64 else 32, block_tables.stride(0),
             _ptr(seq_lens), 0, B, H, num_kv_heads, D, _ptr(out),

@@ -30,7 +30,7 @@ def lib():
 
 def test_every_declared_symbol_is_exported_and_bound(lib):
     names = _declared()
-    assert "slmt_decode_paged" in names and len(names) >= 9
+    assert {"slmt_decode_paged", "slmt_decode_paged_batched"} <= set(names) and len(names) >= 10
     out = subprocess.run(["nm", "-D", "--defined-only", str(_native.library_path())],
                          capture_output=True, text=True, check=True).stdout
     exported = set(re.findall(r"\bT (slmt_[a-z0-9_]+)", out))
@@ -71,9 +71,9 @@ def _paged(lib, **kw):
     a = dict(q=16, qs=4096, qh=128, cache=16, nb=4, bs=16, bt=16, bits=32, bts=4, sl=None, fixed=5,
              B=1, H=32, KV=8, D=128, out=16, od=_native.OUT_F32, os_=4096, oh=128, ws=None, wsb=0)
     a.update(kw)
-    return lib.slmt_decode_paged(a["q"], a["qs"], a["qh"], a["cache"], a["nb"], a["bs"], a["bt"], a["bits"],
-                                 a["bts"], a["sl"], a["fixed"], a["B"], a["H"], a["KV"], a["D"], a["out"],
-                                 a["od"], a["os_"], a["oh"], a["ws"], a["wsb"], None)
+    return lib.slmt_decode_paged_batched(a["q"], a["qs"], a["qh"], a["cache"], a["nb"], a["bs"], a["bt"],
+                                         a["bits"], a["bts"], a["sl"], a["fixed"], a["B"], a["H"], a["KV"],
+                                         a["D"], a["out"], a["od"], a["os_"], a["oh"], a["ws"], a["wsb"], None)
 
 
 @pytest.mark.parametrize("kw,msg", [
@@ -95,6 +95,17 @@ def test_paged_decode_validation(lib, kw, msg):
 
 def test_empty_batch_is_a_no_op(lib):
     assert _paged(lib, B=0, q=None, out=None) == _native.OK
+
+
+def test_single_request_entry_validates_like_the_reference(lib):
+    """slmt_decode_paged (one request, int64 block row) shares the batched checks."""
+    f = ctypes.c_void_p(16)
+    assert lib.slmt_decode_paged(f, f, 4, 16, f, -1, 32, 8, 128, f, None, 0, None) == _native.ERR_INVALID
+    assert b"seq_len must be >= 0" in lib.slmt_last_error()
+    assert lib.slmt_decode_paged(f, f, 4, 16, f, 5, 32, 8, 80 + 16, f, None, 0, None) == _native.ERR_INVALID
+    assert b"head_dim must be 64/80/128" in lib.slmt_last_error()
+    assert lib.slmt_decode_paged(f, f, 4, 16, f, 5, 30, 8, 128, f, None, 0, None) == _native.ERR_INVALID
+    assert b"H not divisible by num_kv_heads" in lib.slmt_last_error()
 
 
 def test_store_and_quantizer_validation(lib):
