@@ -2,6 +2,8 @@
 // dispatch.  Nothing here allocates device memory.
 #include "attention_kernel.h"
 
+#include <algorithm>
+
 namespace slmt {
 
 namespace {
@@ -69,7 +71,21 @@ int plan_attention(int B, int H, int G, int D, int dma_kv, AttnPlan* plan) {
   plan->W_ws = plan->W;
   plan->dma = false;
   plan->lds_bytes = lds;
+  plan->rows = false;
+  plan->rows_nkv = plan->rows_wpk = plan->rows_groups = 0;
   if (dma_kv <= 0) return SLMT_OK;
+
+  // Whole-row kernel first: it covers head_dim 128 with 4 or 8 query heads per
+  // KV head.  The workspace is sized for the larger of its grid and the
+  // other plans' (W_ws).
+  int nkv, wpk, rgroups;
+  if (rows_shape(H, G, D, dma_kv, &nkv, &wpk, &rgroups)) {
+    plan->rows = true;
+    plan->rows_nkv = nkv;
+    plan->rows_wpk = wpk;
+    plan->rows_groups = rgroups;
+    plan->W_ws = std::max(plan->W_ws, rows_max_workgroups(nkv, wpk, rgroups, cus));
+  }
 
   // Direct-load plan: every wave's 4 heads share one KV head (G % 4 == 0) and
   // cache rows are a multiple of 16 bytes (an even number of KV heads), so a
@@ -86,6 +102,7 @@ int plan_attention(int B, int H, int G, int D, int dma_kv, AttnPlan* plan) {
   plan->dma = true;
   plan->lds_bytes = (size_t)geo.total;
   if (plan->W > plan->W_ws) plan->W_ws = plan->W;
+  if (plan->rows) plan->W_ws = std::max(plan->W_ws, rows_max_workgroups(nkv, wpk, rgroups, cus));
   return SLMT_OK;
 }
 
@@ -96,7 +113,7 @@ int64_t attention_workspace_bytes(int B, int H, int KV, int D) {
   }
   AttnPlan pl;
   if (plan_attention(B, H, H / KV, D, KV, &pl) != SLMT_OK) return -1;
-  if ((int64_t)pl.groups * B > kCounterCap) {
+  if ((int64_t)std::max(pl.groups, pl.rows_groups) * B > kCounterCap) {
     fail(SLMT_ERR_UNSUPPORTED, "attention: more than 2^20 (sequence, head group) pairs in one call");
     return -1;
   }
@@ -113,7 +130,8 @@ int launch_attention(int mode, int D, AttnParams& p, void* workspace, int64_t ws
   AttnPlan pl;
   int rc = plan_attention(p.B, p.H, p.G, D, dma_ok ? p.cache_kv : 0, &pl);
   if (rc != SLMT_OK) return rc;
-  if ((int64_t)pl.groups * p.B > kCounterCap)
+  const int groups = pl.rows ? std::max(pl.groups, pl.rows_groups) : pl.groups;
+  if ((int64_t)groups * p.B > kCounterCap)
     return fail(SLMT_ERR_UNSUPPORTED, "attention: more than 2^20 (sequence, head group) pairs in one call");
   const WsLayout lay = ws_layout(pl, p.B, p.H, D);
   if (workspace == nullptr || ws_bytes < lay.total)
@@ -127,6 +145,10 @@ int launch_attention(int mode, int D, AttnParams& p, void* workspace, int64_t ws
   p.W = pl.W;
   p.nthreads = pl.waves * 64;
   if (p.min_tiles <= 0) p.min_tiles = 4;
+  if (mode == SRC_PAGED && pl.rows) {
+    p.W = pl.W_ws;   // the kernel lowers it to the workgroups the CUs hold
+    return launch_attention_rows(pl.rows_nkv, pl.rows_wpk, pl.rows_groups, p, stream);
+  }
   const dim3 grid(pl.W, pl.groups), block(pl.waves * 64);
   if (mode == SRC_PAGED) {
     const bool shared = (p.G % 4) == 0;   // every wave's 4 heads share one KV head

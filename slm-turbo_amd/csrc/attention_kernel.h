@@ -125,7 +125,8 @@ __device__ __forceinline__ void vm_wait_tiles(int ahead) {   // ahead wave-unifo
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
 __device__ __forceinline__ void lds_load16(const void* sbase, uint32_t voff, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(lds)
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase),
+               "s"(__builtin_amdgcn_readfirstlane(lds))
                : "memory", "m0");
 }
 #pragma clang diagnostic pop
@@ -220,6 +221,138 @@ __device__ __forceinline__ int64_t block_of_lane(const AttnParams& p, int b, int
   const int64_t e = (int64_t)b * p.bt_stride + idx;
   if (p.bt64) return reinterpret_cast<const int64_t*>(p.block_tables)[e];
   return reinterpret_cast<const int32_t*>(p.block_tables)[e];
+}
+
+// Stream-K schedule shared by the attention kernels: the concatenated tile
+// list of all sequences (TT tokens per tile) split evenly over the effective
+// workgroup count.  Every thread of the workgroup calls it; it writes zeros
+// for sequences of length 0 (spread over the workgroups, heads [h0, h1)) and
+// returns false when this workgroup has no tiles.  misc: LDS scratch of at
+// least 24 ints.
+struct TileRange {
+  int T, Weff, lo, hi;   // total tiles, workgroups in use, this workgroup's [lo, hi)
+  int b, Pb;             // sequence holding tile lo and its first global tile
+};
+
+template <int TT, int D>
+__device__ bool schedule_range(const AttnParams& p, int* misc, int h0, int h1, TileRange& r) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = uniform(tid >> 6);
+  const int NT = blockDim.x, nwaves = NT >> 6;
+  // exclusive scan of the per-sequence tile counts (threads own contiguous chunks)
+  int my_excl, mysum = 0;
+  const int chunk = (p.B + NT - 1) / NT;
+  const int cb0 = min(p.B, tid * chunk), cb1 = min(p.B, cb0 + chunk);
+  for (int b = cb0; b < cb1; ++b) mysum += tiles_of<TT>(seq_len_lane(p, b));
+  {
+    int v = mysum;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int n = __shfl_up(v, o, 64);
+      if (lane >= o) v += n;
+    }
+    if (lane == 63) misc[wave] = v;
+    lds_barrier();
+    if (tid == 0) {
+      int run = 0;
+      for (int w = 0; w < nwaves; ++w) {
+        const int t = misc[w];
+        misc[w] = run;
+        run += t;
+      }
+      misc[nwaves] = run;
+    }
+    lds_barrier();
+    my_excl = v - mysum + misc[wave];
+    r.T = uniform(misc[nwaves]);
+  }
+  r.Weff = max(1, min(p.W, (r.T + p.min_tiles - 1) / p.min_tiles));
+  const int wg = blockIdx.x;
+  if (wg >= r.Weff) return false;
+  for (int b = wg; b < p.B; b += r.Weff) {
+    if (seq_len_of(p, b) == 0) {
+      for (int e = tid; e < (h1 - h0) * D; e += NT) {
+        const int h = h0 + e / D, d = e % D;
+        const int64_t o = (int64_t)b * p.out_seq_stride + (int64_t)h * p.out_head_stride + d;
+        if (p.out_f16) reinterpret_cast<uint16_t*>(p.out)[o] = 0;
+        else reinterpret_cast<float*>(p.out)[o] = 0.0f;
+      }
+    }
+  }
+  if (r.T == 0) return false;
+  r.lo = range_start(wg, r.T, r.Weff);
+  r.hi = range_start(wg + 1, r.T, r.Weff);
+  // locate the sequence holding tile lo
+  if (r.lo >= my_excl && r.lo < my_excl + mysum) {
+    int run = my_excl;
+    for (int b = cb0; b < cb1; ++b) {
+      const int t = tiles_of<TT>(seq_len_lane(p, b));
+      if (r.lo < run + t) {
+        misc[20] = b;
+        misc[21] = run;
+        break;
+      }
+      run += t;
+    }
+  }
+  lds_barrier();
+  r.b = uniform(misc[20]);
+  r.Pb = uniform(misc[21]);
+  return true;
+}
+
+// Last-arriver merge of sequence b (tiles [Pb, Pb + Tb) of T over Weff
+// workgroups): combines the (m, l, o) partials of every piece, in one pass
+// with a running maximum, and writes the output of heads [h0, h1).  Pieces
+// are read agent-coherently after the arrival counter showed that all of
+// them were published.  For the per-channel layout the V scale/zero are
+// applied to the merged average.
+template <int D, int MODE>
+__device__ void merge_sequence(const AttnParams& p, int b, int Pb, int Tb, int T, int Weff, int h0, int h1,
+                               int group) {
+  const int tid = threadIdx.x, NT = blockDim.x, G = p.G;
+  const int w_first = range_owner(Pb, T, Weff);
+  const int w_last = range_owner(Pb + Tb - 1, T, Weff);
+  const int first_slot = (range_start(w_first, T, Weff) == Pb) ? 0 : 1;
+  // 4 consecutive dims per work item
+  for (int e = tid; e < (h1 - h0) * (D / 4); e += NT) {
+    const int h = h0 + e / (D / 4), d = (e - (e / (D / 4)) * (D / 4)) * 4;
+    float M = -INFINITY, Lsum = 0.f;
+    float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll 2
+    for (int w = w_first; w <= w_last; ++w) {
+      const int s = (w == w_first) ? first_slot : 0;
+      const int64_t base = ((int64_t)w * 2 + s) * p.H + h;
+      const float2 ml = load_pair_agent(p.part_ml + base * 2);
+      const float2 o01 = load_pair_agent(p.part_o + base * D + d);
+      const float2 o23 = load_pair_agent(p.part_o + base * D + d + 2);
+      const float Mn = fmaxf(M, ml.x);
+      const float a = __builtin_amdgcn_exp2f(M - Mn);        // 0 for the first piece (M = -inf)
+      const float sc = __builtin_amdgcn_exp2f(ml.x - Mn);
+      Lsum = Lsum * a + sc * ml.y;
+      O.x = O.x * a + sc * o01.x;
+      O.y = O.y * a + sc * o01.y;
+      O.z = O.z * a + sc * o23.x;
+      O.w = O.w * a + sc * o23.y;
+      M = Mn;
+    }
+    const float rL = __builtin_amdgcn_rcpf(Lsum);
+    float r[4] = {O.x * rL, O.y * rL, O.z * rL, O.w * rL};
+    if constexpr (MODE == SRC_CHANNEL) {
+      if (p.use_quant) {
+        const int64_t kvg = h / G;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) r[k] = h2f(p.vr0[kvg * D + d + k]) * (r[k] - h2f(p.vr1[kvg * D + d + k]));
+      }
+    }
+    const int64_t off = (int64_t)b * p.out_seq_stride + (int64_t)h * p.out_head_stride + d;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      if (p.out_f16) reinterpret_cast<uint16_t*>(p.out)[off + k] = f2h(r[k]);
+      else reinterpret_cast<float*>(p.out)[off + k] = r[k];
+    }
+  }
+  if (tid == 0)
+    __hip_atomic_store(p.counters + (int64_t)group * p.B + b, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Tile loader of the general path: chunk c of a tile is 8 bytes; a thread
@@ -653,69 +786,13 @@ __global__ void __launch_bounds__(MAX_THREADS) attention_kernel(const AttnParams
   int* misc = reinterpret_cast<int*>(smem + (DMA ? dgeo.misc : geo.misc));
 
   // ---------------------------------------------------------------- schedule
-  // Exclusive scan of the per-sequence tile counts (threads own contiguous chunks).
-  int T, my_excl, mysum = 0;
-  const int chunk = (p.B + NT - 1) / NT;
-  const int cb0 = min(p.B, tid * chunk), cb1 = min(p.B, cb0 + chunk);
-  for (int b = cb0; b < cb1; ++b) mysum += tiles_of<TT>(seq_len_lane(p, b));
-  {
-    int v = mysum;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const int n = __shfl_up(v, o, 64);
-      if (lane >= o) v += n;
-    }
-    if (lane == 63) misc[wave] = v;
-    lds_barrier();
-    if (tid == 0) {
-      int run = 0;
-      for (int w = 0; w < nwaves; ++w) {
-        const int t = misc[w];
-        misc[w] = run;
-        run += t;
-      }
-      misc[nwaves] = run;
-    }
-    lds_barrier();
-    my_excl = v - mysum + misc[wave];
-    T = uniform(misc[nwaves]);
-  }
-  const int Weff = max(1, min(p.W, (T + p.min_tiles - 1) / p.min_tiles));
+  TileRange rng;
+  if (!schedule_range<TT, D>(p, misc, h0, h1, rng)) return;
+  const int T = rng.T, Weff = rng.Weff, lo = rng.lo, hi = rng.hi;
   const int wg = blockIdx.x;
-  if (wg >= Weff) return;
-
-  // Sequences of length 0 produce zeros (spread over the workgroups).
-  for (int b = wg; b < p.B; b += Weff) {
-    if (seq_len_of(p, b) == 0) {
-      for (int e = tid; e < (h1 - h0) * D; e += NT) {
-        const int h = h0 + e / D, d = e % D;
-        const int64_t o = (int64_t)b * p.out_seq_stride + (int64_t)h * p.out_head_stride + d;
-        if (p.out_f16) reinterpret_cast<uint16_t*>(p.out)[o] = 0;
-        else reinterpret_cast<float*>(p.out)[o] = 0.0f;
-      }
-    }
-  }
-  if (T == 0) return;
-  const int lo = range_start(wg, T, Weff);
-  const int hi = range_start(wg + 1, T, Weff);
-
-  // Locate the sequence holding tile lo.
-  if (lo >= my_excl && lo < my_excl + mysum) {
-    int run = my_excl;
-    for (int b = cb0; b < cb1; ++b) {
-      const int t = tiles_of<TT>(seq_len_lane(p, b));
-      if (lo < run + t) {
-        misc[20] = b;
-        misc[21] = run;
-        break;
-      }
-      run += t;
-    }
-  }
-  lds_barrier();
   Cursor cc;
-  cc.b = uniform(misc[20]);
-  cc.Pb = uniform(misc[21]);
+  cc.b = rng.b;
+  cc.Pb = rng.Pb;
   cc.Lb = seq_len_of(p, cc.b);
   cc.Tb = tiles_of<TT>(cc.Lb);
   cc.tb = lo - cc.Pb;
@@ -1011,54 +1088,8 @@ __global__ void __launch_bounds__(MAX_THREADS) attention_kernel(const AttnParams
     misc[25] = npend > 1 ? arrive(pb1, pP1, pT1) : 0;
   }
   __syncthreads();
-  // The last piece to arrive merges every piece of the sequence, in one pass
-  // with a running maximum (pieces are read agent-coherently, after the
-  // counter showed that all of them were published).
-  auto merge = [&](int b, int Pb, int Tb) {
-    const int w_first = range_owner(Pb, T, Weff);
-    const int w_last = range_owner(Pb + Tb - 1, T, Weff);
-    const int first_slot = (range_start(w_first, T, Weff) == Pb) ? 0 : 1;
-    // 4 consecutive dims per work item
-    for (int e = tid; e < (h1 - h0) * (D / 4); e += NT) {
-      const int h = h0 + e / (D / 4), d = (e - (e / (D / 4)) * (D / 4)) * 4;
-      float M = -INFINITY, Lsum = 0.f;
-      float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll 2
-      for (int w = w_first; w <= w_last; ++w) {
-        const int s = (w == w_first) ? first_slot : 0;
-        const int64_t base = ((int64_t)w * 2 + s) * p.H + h;
-        const float2 ml = load_pair_agent(p.part_ml + base * 2);
-        const float2 o01 = load_pair_agent(p.part_o + base * D + d);
-        const float2 o23 = load_pair_agent(p.part_o + base * D + d + 2);
-        const float Mn = fmaxf(M, ml.x);
-        const float a = __builtin_amdgcn_exp2f(M - Mn);        // 0 for the first piece (M = -inf)
-        const float sc = __builtin_amdgcn_exp2f(ml.x - Mn);
-        Lsum = Lsum * a + sc * ml.y;
-        O.x = O.x * a + sc * o01.x;
-        O.y = O.y * a + sc * o01.y;
-        O.z = O.z * a + sc * o23.x;
-        O.w = O.w * a + sc * o23.y;
-        M = Mn;
-      }
-      const float rL = __builtin_amdgcn_rcpf(Lsum);
-      float r[4] = {O.x * rL, O.y * rL, O.z * rL, O.w * rL};
-      if constexpr (MODE == SRC_CHANNEL) {
-        if (p.use_quant) {
-          const int64_t kvg = h / G;
-#pragma unroll
-          for (int k = 0; k < 4; ++k) r[k] = h2f(p.vr0[kvg * D + d + k]) * (r[k] - h2f(p.vr1[kvg * D + d + k]));
-        }
-      }
-      const int64_t off = (int64_t)b * p.out_seq_stride + (int64_t)h * p.out_head_stride + d;
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        if (p.out_f16) reinterpret_cast<uint16_t*>(p.out)[off + k] = f2h(r[k]);
-        else reinterpret_cast<float*>(p.out)[off + k] = r[k];
-      }
-    }
-    if (tid == 0)
-      __hip_atomic_store(p.counters + (int64_t)group * p.B + b, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  };
+  // The last piece to arrive merges every piece of the sequence.
+  auto merge = [&](int b, int Pb, int Tb) { merge_sequence<D, MODE>(p, b, Pb, Tb, T, Weff, h0, h1, group); };
   if (misc[24]) merge(pb0, pP0, pT0);
   if (misc[25]) merge(pb1, pP1, pT1);
   (void)VB;

@@ -1,0 +1,610 @@
+// Batched paged 4-bit decode attention for head_dim 128 with 4 or 8 query
+// heads per KV head: the "whole-row" kernel (reference kernel it replaces:
+// kv_dequant_decode_per_token_paged_kernel, kernels/kv_dequant_kernels.cuh:671-801,
+// batched over the whole decode step instead of launched per request).
+//
+// A workgroup owns NKV consecutive KV heads (a 16-byte aligned sub-row of every
+// cache row, NKV * 136 bytes) and their 4*WPK query heads each, one wave per 4
+// query heads.  Tiles are 32 tokens = 32 sub-rows, two contiguous runs of one
+// paged block each.  Work is split stream-K over the concatenated tile list
+// of all sequences, exactly as in attention_kernel.h, and split sequences are
+// merged by the last workgroup to finish a piece.
+//
+// Staging: the workgroup copies each tile with 16-byte direct loads
+// (global_load_lds_dwordx4, no VGPRs) into an LDS ring of NS stages, NS-1
+// tiles ahead; wave w copies rows 32w/W .. 32(w+1)/W, which lie in one paged
+// block.  Every lane chooses its source unit, so the staged rows get an odd
+// number of 16-byte units (the pad unit re-reads the row's last unit): the
+// 16 rows that the QK lanes read at once then fall in 16 different bank
+// groups.  One barrier per tile publishes the stage.
+//
+// QK (lane = token p of 16 x key quarter c of 4; two rounds per tile): the
+// query is quantized once per sequence to 16-bit fixed point and split into
+// four 4-bit limbs; v_dot8_u32_u4 multiplies 8 packed key nibbles by 8 limb
+// nibbles, so keys are never unpacked.  Each lane dots its quarter of the
+// key with all 4 heads; a reduce-scatter over the quad leaves head c's dot in
+// lane c.  q.K = step * q.n + min * sum(q).
+//
+// PV (lane = V dword column c of 16 x token group q of 4): group q takes the
+// token pairs (4q, 4q+1), (4q+2, 4q+3), (16+4q, 17+4q), (18+4q, 19+4q): its
+// rows are 4 apart from the other groups', which with 69-unit rows puts the
+// 4 groups' reads in disjoint banks.  Two tokens' bytes k are packed into one
+// dword (one v_perm_b32) and read as an fp16 pair of subnormals,
+// (lo + 16 hi) * 2^-24, which v_dot2c_f32_f16 multiplies exactly with the fp16
+// weights p * step; a second product with the low nibbles alone (one AND)
+// separates the two dims.  The per-token min enters once per token as
+// sum(p * min).  The 4 groups' partial sums are added at the end of a
+// segment.
+#include "attention_kernel.h"
+
+#include <algorithm>
+#include <map>
+#include <mutex>
+#include <tuple>
+#include <type_traits>
+
+namespace slmt {
+namespace rows {
+
+using namespace attn;
+
+constexpr int D = 128, SLOT = D + 8, KD = D / 8;
+
+template <int NKV, int WPK, int NS>
+struct Shape {
+  static_assert(NKV % 2 == 0, "sub-rows must be a whole number of 16-byte units");
+  static constexpr int WAVES = NKV * WPK;
+  static constexpr int THREADS = WAVES * 64;
+  static constexpr int UPR = NKV * SLOT / 16;   // 16-byte units of a sub-row
+  static constexpr int RP = UPR | 1;            // units of a staged row
+  static constexpr int RSTRIDE = RP * 16;
+  static constexpr int RW = DTILE / WAVES;      // rows copied per wave
+  static_assert(DTILE % WAVES == 0 && RW <= 16, "a wave's rows must lie in one block");
+  static constexpr int WUNITS = RW * RP;
+  static constexpr int NOPS = (WUNITS + 63) / 64;
+  static constexpr int LAST = WUNITS - 64 * (NOPS - 1);   // lanes of the wave's last load
+  static constexpr int STAGE = DTILE * RSTRIDE;
+  static constexpr int QOFF = NS * STAGE;                  // query slots [NS][WAVES] x 1 KB
+  static constexpr int WOFF = QOFF + NS * WAVES * 1024;    // per-wave limb / weight scratch
+  static constexpr int MOFF = WOFF + WAVES * 1024;         // misc ints
+  static constexpr int LDS = MOFF + 32 * 4;
+  static_assert(LDS <= 160 * 1024, "LDS ring too large");
+};
+
+constexpr float kC = 1.4426950408889634f / 11.313708498984761f;   // log2(e) / sqrt(128)
+
+template <int NKV, int WPK, int NS>
+__global__ void __launch_bounds__(NKV * WPK * 64) rows_kernel(const AttnParams p) {
+  using S = Shape<NKV, WPK, NS>;
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = uniform(tid >> 6);
+  const int group = blockIdx.y;
+  const int wg = blockIdx.x;
+  const int h0 = group * 4 * S::WAVES, h1 = h0 + 4 * S::WAVES;   // the host checks H % (4 * WAVES) == 0
+  const int kv_lo = group * NKV;
+  const int kvw = wave / WPK;                                     // the wave's KV head within the group
+  const int hw = h0 + 4 * wave;                                   // the wave's first query head
+  int* misc = reinterpret_cast<int*>(smem + S::MOFF);
+  uint8_t* const wscr = smem + S::WOFF + wave * 1024;
+
+  TileRange rng;
+  if (!schedule_range<DTILE, D>(p, misc, h0, h1, rng)) return;
+  const int T = rng.T, Weff = rng.Weff, lo = rng.lo, hi = rng.hi;
+
+  // ---------------------------------------------------------------- loads
+  // Load i of the wave moves LDS units 64i .. 64i+63 of its run; lane l unit
+  // u = 64i + l = row rw0 + u / RP, column u % RP (the pad column re-reads
+  // column UPR-1).
+  const int cache_row = p.cache_kv * SLOT;
+  const int a0 = kv_lo * SLOT;
+  const int rw0 = wave * S::RW;
+  uint32_t goff[S::NOPS];
+#pragma unroll
+  for (int i = 0; i < S::NOPS; ++i) {
+    const int u = 64 * i + lane;
+    const int r = rw0 + u / S::RP, c = min(u % S::RP, S::UPR - 1);
+    goff[i] = u < S::WUNITS ? (uint32_t)((r & 15) * cache_row + a0 + c * 16) : 0u;
+  }
+  const uint32_t lds_smem = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)smem;
+  const uint32_t lds_run = lds_smem + rw0 * S::RSTRIDE;
+  // query rows: lane (qp, qg) moves dims 8qp .. 8qp+7 of head hw + qg
+  const int qp = lane >> 2, qg = lane & 3;
+  const uint32_t qoff = (uint32_t)(((hw + qg) * p.q_head_stride + qp * 8) * 2);
+
+  // Tile descriptors, 64 tiles at a time, lane i for tile dchunk + i: the base
+  // of this wave's block run and an info word
+  //   sequence << 8 | first tile of the sequence << 7 | last tile << 6 | (valid tokens - 1).
+  // Block-table entries are read as their low 32 bits (num_blocks < 2^31).
+  const int esh = p.bt64 ? 3 : 2;
+  const uint8_t* btab = reinterpret_cast<const uint8_t*>(p.block_tables);
+  const int64_t blk_bytes = (int64_t)p.block_size * cache_row;
+  const int hoff = rw0 >= 16 ? 16 : 0;          // the wave's rows are tokens tok0 + hoff ..
+  uint32_t dlo = 0, dhi = 0;
+  int dinfo = 0, dchunk = lo;
+  int cb = rng.b, cP = rng.Pb;                  // a sequence at or before the next chunk's first tile
+  auto build = [&](int first) {
+    int b = cb, P = cP;
+    int L = seq_len_of(p, b), Tb = tiles_of<DTILE>(L);
+    while (first >= P + Tb && b + 1 < p.B) {
+      P += Tb;
+      ++b;
+      L = seq_len_of(p, b);
+      Tb = tiles_of<DTILE>(L);
+    }
+    cb = b;
+    cP = P;
+    const int t = first + lane;
+    int mb = -1, mtb = 0, mL = 0, mTb = 0;
+    for (;;) {
+      if (t >= P && t < P + Tb) {
+        mb = b;
+        mtb = t - P;
+        mL = L;
+        mTb = Tb;
+      }
+      P += Tb;
+      if (!__builtin_amdgcn_ballot_w64(t >= P && t < hi) || b + 1 >= p.B) break;
+      ++b;
+      L = seq_len_of(p, b);
+      Tb = tiles_of<DTILE>(L);
+    }
+    uint64_t base = reinterpret_cast<uint64_t>(p.cache);
+    dinfo = 0;
+    if (mb >= 0 && t < hi) {
+      const int tok0 = mtb * DTILE;
+      const int tok = tok0 + hoff < mL ? tok0 + hoff : tok0;   // past the end: any valid block
+      const int32_t e =
+          *reinterpret_cast<const int32_t*>(btab + (((int64_t)mb * p.bt_stride + (tok >> p.block_shift)) << esh));
+      base += (uint64_t)(uint32_t)e * (uint64_t)blk_bytes + (uint64_t)((tok & (p.block_size - 1)) * cache_row);
+      dinfo = (mb << 8) | ((mtb == 0) << 7) | ((mtb == mTb - 1) << 6) | (min(DTILE, mL - tok0) - 1);
+    }
+    dlo = (uint32_t)base;
+    dhi = (uint32_t)(base >> 32);
+    dchunk = first;
+  };
+  // Issues tile t into ring stage st; returns its info word.
+  auto issue = [&](int t, int st) -> int {
+    const int i = t - dchunk;
+    const uint8_t* base = reinterpret_cast<const uint8_t*>((uint64_t)readlane_u32(dlo, i) |
+                                                           ((uint64_t)readlane_u32(dhi, i) << 32));
+    const int info = __builtin_amdgcn_readlane(dinfo, i);
+    const uint32_t dst = lds_run + st * S::STAGE;
+#pragma unroll
+    for (int k = 0; k < S::NOPS; ++k) {
+      if (k < S::NOPS - 1 || S::LAST == 64 || lane < S::LAST) lds_load16(base, goff[k], dst + k * 1024);
+    }
+    if (((info >> 7) & 1) || t == lo)
+      lds_load16(p.q + (int64_t)(info >> 8) * p.q_seq_stride, qoff, lds_smem + S::QOFF + (st * S::WAVES + wave) * 1024);
+    return info;
+  };
+
+  // ---------------------------------------------------------------- per-wave state
+  // QK lane (token p, key quarter qc = lane & 3): limbs of all 4 heads for
+  // the lane's 4 key dwords, in the order the lane reads them (odd quarters
+  // read their two 8-byte halves swapped, so the quad covers all 32 banks)
+  uint32_t qlq[4][4][4];              // [head][dword][limb]
+  float qa = 0.f, qb = 0.f, m_run = -INFINITY, l_run = 0.f, vmt = 0.f;
+  float accl[4][4], accf[4][4];       // [byte k][head]: sum w * lo, sum w * (lo + 16 hi), units of 2^-24
+  const int pc = lane & 15, pq = lane >> 4;   // PV: dword column, token group
+
+  auto begin = [&](const uint8_t* qlds) {
+    m_run = -INFINITY;
+    l_run = 0.f;
+    vmt = 0.f;
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+#pragma unroll
+      for (int h = 0; h < 4; ++h) accl[k][h] = accf[k][h] = 0.f;
+    const uint4 w = *reinterpret_cast<const uint4*>(qlds + lane * 16);
+    const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+    float qv[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      qv[2 * i] = h2f((uint16_t)(ws[i] & 0xffffu));
+      qv[2 * i + 1] = h2f((uint16_t)(ws[i] >> 16));
+    }
+    float amax = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(qv[i]));
+    amax = red16_max(amax);
+    // scale to 16-bit fixed point; the score below uses the same reciprocal
+    // of it throughout, so it is exact for the quantized query qi * rsq
+    const float sq = amax > 0.f ? 32767.0f * __builtin_amdgcn_rcpf(amax) : 1.0f;
+    const float rsq = __builtin_amdgcn_rcpf(sq);
+    // The nibble dot and sum(q) both use qi.
+    uint32_t limb[4] = {0u, 0u, 0u, 0u};
+    int isum = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      int qi = (int)__builtin_rintf(qv[i] * sq);
+      qi = max(-32767, min(32767, qi));
+      isum += qi;
+      const uint32_t qu = (uint32_t)(qi + 32768);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) limb[k] |= ((qu >> (4 * k)) & 15u) << (4 * i);
+    }
+    const float qsum = red16_sum((float)isum) * rsq;    // |sum qi| < 2^24: exact before the scaling
+    uint32_t* wl = reinterpret_cast<uint32_t*>(wscr);
+    wave_lds_sync();                     // earlier weight reads of this wave are done
+#pragma unroll
+    for (int k = 0; k < 4; ++k) wl[(qg * 4 + k) * 16 + qp] = limb[k];
+    wave_lds_sync();
+    // (head h, limb k) words 4qc .. 4qc+3 of this lane's quarter
+    const bool swp = qg & 1;
+#pragma unroll
+    for (int h = 0; h < 4; ++h)
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const uint4 v = *reinterpret_cast<const uint4*>(wl + (h * 4 + k) * 16 + 4 * qg);
+        qlq[h][0][k] = swp ? v.z : v.x;
+        qlq[h][1][k] = swp ? v.w : v.y;
+        qlq[h][2][k] = swp ? v.x : v.z;
+        qlq[h][3][k] = swp ? v.y : v.w;
+      }
+    qa = kC * rsq;
+    qb = kC * qsum;
+  };
+
+  // Score of this lane's token for head qg (base-2 units): the lane's key
+  // quarter kq against all 4 heads' limbs, the quad's partial dots added by a
+  // reduce-scatter that leaves head c's sum in lane c; kr: the token's rulers.
+  auto score = [&](const uint32_t (&kq)[4], uint2 kr) -> float {
+    uint32_t a[4][4];
+#pragma unroll
+    for (int h = 0; h < 4; ++h)
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        uint32_t x = 0;
+#pragma unroll
+        for (int d = 0; d < 4; ++d) x = __builtin_amdgcn_udot8(kq[d], qlq[h][d][k], x, false);
+        a[h][k] = x;
+      }
+    uint32_t part[4];
+#pragma unroll
+    for (int h = 0; h < 4; ++h) part[h] = a[h][0] + (a[h][1] << 4) + (a[h][2] << 8) + (a[h][3] << 12);
+    // nibble sum of the token: the quad's quarters
+    uint32_t sn = 0;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) sn = __builtin_amdgcn_udot8(kq[d], 0x11111111u, sn, false);
+    sn += dpp_u<DPP_QUAD_XOR1>(sn);
+    sn += dpp_u<DPP_QUAD_XOR2>(sn);
+    // reduce-scatter over the quad: lane c ends with head c
+    const bool o1 = qg & 1, o2 = qg & 2;
+    const uint32_t ya = (o1 ? part[1] : part[0]) + dpp_u<DPP_QUAD_XOR1>(o1 ? part[0] : part[1]);
+    const uint32_t yb = (o1 ? part[3] : part[2]) + dpp_u<DPP_QUAD_XOR1>(o1 ? part[2] : part[3]);
+    const uint32_t z = (o2 ? yb : ya) + dpp_u<DPP_QUAD_XOR2>(o2 ? ya : yb);
+    const int iacc = (int)z - (int)(sn << 15);
+    const float kmin = h2f((uint16_t)(kr.x & 0xffffu));
+    const float kstep = h2f((uint16_t)(kr.x >> 16));
+    return ((float)iacc * qa) * kstep + kmin * qb;
+  };
+
+  // LDS reads of tile data for this lane: its key quarter and rulers of its
+  // two QK tokens, and its 8 V words (PV, used one iteration later).
+  auto read_tile = [&](const uint8_t* Sb, uint32_t (&kq)[2][4], uint2 (&kr)[2], uint32_t (&xv)[8]) {
+    const int sw = (qg & 1) * 8;
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const uint8_t* kb = Sb + (16 * r + qp) * S::RSTRIDE;
+      const uint2 k01 = *reinterpret_cast<const uint2*>(kb + 16 * qg + sw);
+      const uint2 k23 = *reinterpret_cast<const uint2*>(kb + 16 * qg + 8 - sw);
+      kq[r][0] = k01.x;
+      kq[r][1] = k01.y;
+      kq[r][2] = k23.x;
+      kq[r][3] = k23.y;
+      kr[r] = *reinterpret_cast<const uint2*>(kb + D);
+    }
+    const uint8_t* vb = Sb + D / 2 + 4 * pc;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int P = (j < 2 ? 2 * pq + j : 8 + 2 * pq + j - 2);   // token pair (2P, 2P+1)
+      xv[2 * j] = *reinterpret_cast<const uint32_t*>(vb + (2 * P) * S::RSTRIDE);
+      xv[2 * j + 1] = *reinterpret_cast<const uint32_t*>(vb + (2 * P + 1) * S::RSTRIDE);
+    }
+  };
+
+  // QK and softmax of one tile; its fp16 weights go to the scratch half `wh`
+  // (256 bytes: dword [pair][head] = (w(2i), w(2i+1))).
+  auto qk_softmax = [&](const uint32_t (&kq)[2][4], const uint2 (&kr)[2], int nvalid, uint8_t* wh) {
+    float s2[2];
+    bool tv[2];
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      tv[r] = 16 * r + qp < nvalid;
+      const float sc = score(kq[r], kr[r]);
+      s2[r] = tv[r] ? sc : -INFINITY;
+    }
+    // online softmax: the running max per head is only recomputed (and the
+    // sums rescaled) when some score of the tile exceeds it
+    if (__builtin_amdgcn_ballot_w64(s2[0] > m_run || s2[1] > m_run)) {
+      const float tmax = red16_max(fmaxf(s2[0], s2[1]));
+      const bool grow = tmax > m_run;
+      const float alpha = grow ? __builtin_amdgcn_exp2f(m_run - tmax) : 1.f;   // 0 when growing from -inf
+      l_run *= alpha;
+      vmt *= alpha;
+#pragma unroll
+      for (int h = 0; h < 4; ++h) {
+        const float ah = readlane_f(alpha, h);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          accl[k][h] *= ah;
+          accf[k][h] *= ah;
+        }
+      }
+      m_run = grow ? tmax : m_run;
+    }
+    uint16_t* w16 = reinterpret_cast<uint16_t*>(wh);
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      // m_run > -inf here: token 0 of every tile is valid
+      const float pr = __builtin_amdgcn_exp2f(s2[r] - m_run);
+      const float vmin = h2f((uint16_t)(kr[r].y & 0xffffu));
+      const float vstep = h2f((uint16_t)(kr[r].y >> 16));
+      l_run += tv[r] ? pr : 0.f;
+      vmt += tv[r] ? pr * vmin : 0.f;
+      const int tok = 16 * r + qp;
+      w16[((tok >> 1) * 4 + qg) * 2 + (tok & 1)] = f2h(tv[r] ? pr * vstep : 0.f);
+    }
+  };
+
+  // PV of one tile from its V words and the weights in scratch half `wh`.
+  auto pv = [&](const uint32_t (&xv)[8], const uint8_t* wh) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int P = (j < 2 ? 2 * pq + j : 8 + 2 * pq + j - 2);
+      const uint4 wq = *reinterpret_cast<const uint4*>(wh + P * 16);
+      const uint32_t whd[4] = {wq.x, wq.y, wq.z, wq.w};
+      const uint32_t x0 = xv[2 * j], x1 = xv[2 * j + 1];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        // byte k of both tokens at bits 0-7 and 16-23
+        const uint32_t tw = __builtin_amdgcn_perm(x1, x0, 0x0C000C00u | ((4u + k) << 16) | (uint32_t)k);
+        const uint32_t vlo = tw & 0x000F000Fu;
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+          accl[k][h] = fdot2(whd[h], vlo, accl[k][h]);
+          accf[k][h] = fdot2(whd[h], tw, accf[k][h]);
+        }
+      }
+    }
+  };
+
+  // Pending partial pieces, counted after the range (at most two: the range's
+  // first and last segments): sequence, first tile, tiles.
+  int npend = 0;
+  int pb0 = 0, pP0 = 0, pT0 = 0, pb1 = 0, pP1 = 0, pT1 = 0;
+
+  // End of a segment of sequence b whose first tile is seg_first (a whole
+  // sequence when `whole`): add the token groups' sums and write the output
+  // or a partial piece.
+  auto finish = [&](int b, int seg_first, bool whole, bool last_of_seq) {
+    const float lt = red16_sum(l_run);   // lane g: head g
+    const float vt = red16_sum(vmt);
+    // Sum every accumulator over the 4 token groups (rows of 16 lanes).  The
+    // four values (head h, lo|full, byte k = 0..3) are folded together: two
+    // permlane16 swaps and one permlane32 swap leave the total of byte k in
+    // row k.  Lane (pc, row pq) then owns dims 8pc + 2pq and 8pc + 2pq + 1.
+    float o[4][2];                       // [head][dim 8pc + 2pq + i], un-normalized
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+      float r[2];
+#pragma unroll
+      for (int x = 0; x < 2; ++x) {
+        float v0 = x ? accf[0][h] : accl[0][h], v1 = x ? accf[1][h] : accl[1][h];
+        float v2 = x ? accf[2][h] : accl[2][h], v3 = x ? accf[3][h] : accl[3][h];
+        permlane16_swap_pair(v0, v1);    // v0 + v1: rows [b0 r01, b1 r01, b0 r23, b1 r23]
+        permlane16_swap_pair(v2, v3);
+        float s01 = v0 + v1, s23 = v2 + v3;
+        permlane32_swap_pair(s01, s23);  // s01 + s23: row k holds byte k's total
+        r[x] = s01 + s23;
+      }
+      const float vh = readlane_f(vt, h);
+      o[h][0] = r[0] * 16777216.0f + vh;            // 2^24: nibble-as-subnormal scale
+      o[h][1] = (r[1] - r[0]) * 1048576.0f + vh;    // (16 hi) * 2^-24 -> hi
+    }
+    const int dcol = 8 * pc + 2 * pq;
+    if (whole && last_of_seq) {
+#pragma unroll
+      for (int h = 0; h < 4; ++h) {
+        const float rL = __builtin_amdgcn_rcpf(readlane_f(lt, h));
+        const int64_t off = (int64_t)b * p.out_seq_stride + (int64_t)(hw + h) * p.out_head_stride + dcol;
+        if (p.out_f16) {
+          *reinterpret_cast<uint32_t*>(reinterpret_cast<uint16_t*>(p.out) + off) =
+              (uint32_t)f2h(o[h][0] * rL) | ((uint32_t)f2h(o[h][1] * rL) << 16);
+        } else {
+          *reinterpret_cast<float2*>(reinterpret_cast<float*>(p.out) + off) = make_float2(o[h][0] * rL, o[h][1] * rL);
+        }
+      }
+    } else {
+      // partial piece: slot 0 when this segment is the range's first, else 1
+      const int slot = (seg_first == lo) ? 0 : 1;
+      const int64_t pbase = ((int64_t)wg * 2 + slot) * p.H;
+#pragma unroll
+      for (int h = 0; h < 4; ++h) store_pair_agent(p.part_o + (pbase + hw + h) * D + dcol, o[h][0], o[h][1]);
+      if (lane < 4) store_pair_agent(p.part_ml + (pbase + hw + lane) * 2, m_run, lt);   // lane g: head g
+      const int L = seq_len_of(p, b);
+      const int Pb = whole ? seg_first : rng.Pb;
+      if (npend == 0) {
+        pb0 = b;
+        pP0 = Pb;
+        pT0 = tiles_of<DTILE>(L);
+      } else {
+        pb1 = b;
+        pP1 = Pb;
+        pT1 = tiles_of<DTILE>(L);
+      }
+      ++npend;
+    }
+  };
+
+  // ---------------------------------------------------------------- pipeline
+  // Tiles lo .. lo+NS-2 are issued up front; iteration t waits for this
+  // wave's loads of tile t, meets the other waves at a barrier (tile t is then
+  // complete in LDS and every wave is done with tile t-1), and issues tile
+  // t+NS-1 into the stage tile t-1 used.  Compute is software-pipelined one
+  // tile deep: iteration t reads tile t's data from LDS, runs PV of tile t-1
+  // (V words kept in registers, weights in that tile's scratch slot) while
+  // those reads land, then QK and softmax of tile t.  A segment that ends at
+  // tile t-1 is finished right after its PV.  The loop is unrolled by NS, so
+  // stage numbers are constants: tile lo + j uses stage and weight slot j % NS.
+  build(lo);
+  int sinfo[NS];                // info of the tile in each stage
+#pragma unroll
+  for (int j = 0; j < NS; ++j) sinfo[j] = 0;
+#pragma unroll
+  for (int j = 0; j < NS - 1; ++j)
+    if (lo + j < hi) sinfo[j] = issue(lo + j, j);
+  int seg_first = lo;
+  bool seg_whole = false;
+  uint32_t xvp[8];              // V words of the previous tile
+  int pinfo = 0;                // info of the previous tile
+#pragma unroll
+  for (int i = 0; i < 8; ++i) xvp[i] = 0;
+
+  auto iteration = [&](int t, auto stage) {
+    constexpr int st = decltype(stage)::value;
+    constexpr int sprev = (st + NS - 1) % NS;
+    // tiles t+1 .. t+NS-2 may still be in flight, NOPS loads each (query
+    // loads among them only make the bound stricter); near the end of the
+    // range fewer follow and the wait is for everything
+    if (t + NS - 2 < hi) vm_wait_n<S::NOPS * (NS - 2)>();
+    else vm_wait_n<0>();
+    lds_barrier();
+    const int info = sinfo[st];
+    const int tn = t + NS - 1;
+    if (tn < hi) {
+      if (tn - dchunk >= 64) build(tn);
+      sinfo[sprev] = issue(tn, sprev);
+    }
+    uint32_t kq[2][4], xv[8];
+    uint2 kr[2];
+    read_tile(smem + st * S::STAGE + kvw * SLOT, kq, kr, xv);
+    if (t > lo) {
+      pv(xvp, wscr + sprev * 256);
+      if ((pinfo >> 6) & 1) finish(pinfo >> 8, seg_first, seg_whole, true);
+    }
+    const bool first_of_seq = (info >> 7) & 1;
+    if (t == lo || first_of_seq) {
+      seg_first = t;
+      seg_whole = first_of_seq;
+      begin(smem + S::QOFF + (st * S::WAVES + wave) * 1024);
+    }
+    qk_softmax(kq, kr, (info & 63) + 1, wscr + st * 256);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) xvp[i] = xv[i];
+    pinfo = info;
+  };
+  static_assert(NS >= 2 && NS <= 4, "one unrolled step per ring stage");
+  for (int t = lo; t < hi; t += NS) {
+    iteration(t, std::integral_constant<int, 0>{});
+    if (t + 1 < hi) iteration(t + 1, std::integral_constant<int, 1>{});
+    if constexpr (NS > 2) { if (t + 2 < hi) iteration(t + 2, std::integral_constant<int, 2 % NS>{}); }
+    if constexpr (NS > 3) { if (t + 3 < hi) iteration(t + 3, std::integral_constant<int, 3 % NS>{}); }
+  }
+  // the range's last tile: its weights are in this wave's scratch (the wave's
+  // own LDS writes are ordered before its reads)
+  wave_lds_sync();
+  pv(xvp, wscr + ((hi - 1 - lo) % NS) * 256);
+  finish(pinfo >> 8, seg_first, seg_whole, (pinfo >> 6) & 1);
+
+  // ---------------------------------------------------------------- arrivals and merges
+  if (npend == 0) return;
+  vm_drain();       // this wave's partial stores are complete (agent-coherent)
+  __syncthreads();
+  auto arrive = [&](int b, int Pb, int Tb) -> int {
+    const int pieces = range_owner(Pb + Tb - 1, T, Weff) - range_owner(Pb, T, Weff) + 1;
+    const int prev = __hip_atomic_fetch_add(p.counters + (int64_t)group * p.B + b, 1, __ATOMIC_RELAXED,
+                                            __HIP_MEMORY_SCOPE_AGENT);
+    return (prev == pieces - 1) ? 1 : 0;
+  };
+  if (tid == 0) {
+    misc[24] = arrive(pb0, pP0, pT0);
+    misc[25] = npend > 1 ? arrive(pb1, pP1, pT1) : 0;
+  }
+  __syncthreads();
+  if (misc[24]) merge_sequence<D, SRC_PAGED>(p, pb0, pP0, pT0, T, Weff, h0, h1, group);
+  if (misc[25]) merge_sequence<D, SRC_PAGED>(p, pb1, pP1, pT1, T, Weff, h0, h1, group);
+}
+
+// Workgroups one CU holds at once (cached per kernel; 0 if unknown).
+static int blocks_per_cu(const void* kern, int threads, size_t lds) {
+  static std::mutex mu;
+  static std::map<std::tuple<const void*, int, size_t>, int> cache;
+  const auto key = std::make_tuple(kern, threads, lds);
+  std::lock_guard<std::mutex> lock(mu);
+  auto it = cache.find(key);
+  if (it != cache.end()) return it->second;
+  (void)hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+  int n = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kern, threads, lds) != hipSuccess) n = 0;
+  (void)hipGetLastError();
+  cache[key] = n;
+  return n;
+}
+
+template <int NKV, int WPK, int NS>
+static int launch(AttnParams p, int groups, hipStream_t stream) {
+  using S = Shape<NKV, WPK, NS>;
+  auto kern = rows_kernel<NKV, WPK, NS>;
+  const int per_cu = blocks_per_cu(reinterpret_cast<const void*>(kern), S::THREADS, S::LDS);
+  const int cus = device_cu_count();
+  int W = std::max(1, cus * std::max(1, per_cu) / groups);
+  if (W > p.W) W = p.W;          // the workspace holds partials for p.W workgroups
+  p.W = W;
+  p.nthreads = S::THREADS;
+  p.heads_per_group = 4 * S::WAVES;
+  hipLaunchKernelGGL(kern, dim3(W, groups), dim3(S::THREADS), S::LDS, stream, p);
+  return check_launch("paged decode");
+}
+
+}  // namespace rows
+
+// Shape of the whole-row kernel for a request, or false if it does not apply.
+bool rows_shape(int H, int G, int D, int cache_kv, int* nkv, int* wpk, int* groups) {
+  if (D != rows::D || (G != 4 && G != 8) || H % G != 0) return false;
+  const int KV = H / G;
+  if (cache_kv != KV || cache_kv % 2 != 0) return false;
+  const int w = G / 4;
+  int n = 0;
+  if (w == 1) n = KV % 8 == 0 ? 8 : KV % 4 == 0 ? 4 : KV % 2 == 0 ? 2 : 0;
+  else n = KV % 4 == 0 ? 4 : KV % 2 == 0 ? 2 : 0;
+  if (n == 0) return false;
+  *nkv = n;
+  *wpk = w;
+  *groups = KV / n;
+  return true;
+}
+
+// Workgroups per head group the whole-row kernel may use (its workspace bound).
+int rows_max_workgroups(int nkv, int wpk, int groups, int cus) {
+  const int waves = nkv * wpk;
+  // at most 8 waves per CU (up to 256 VGPRs each), and the ring's LDS
+  size_t lds = 0;
+  switch (nkv * 10 + wpk) {
+    case 81: lds = rows::Shape<8, 1, 3>::LDS; break;
+    case 41: lds = rows::Shape<4, 1, 4>::LDS; break;
+    case 21: lds = rows::Shape<2, 1, 4>::LDS; break;
+    case 42: lds = rows::Shape<4, 2, 4>::LDS; break;
+    case 22: lds = rows::Shape<2, 2, 4>::LDS; break;
+    default: return 1;
+  }
+  int per_cu = std::min(8 / waves, (int)((160 * 1024) / lds));
+  per_cu = std::max(1, per_cu);
+  return std::max(1, cus * per_cu / groups);
+}
+
+int launch_attention_rows(int nkv, int wpk, int groups, const AttnParams& p, hipStream_t stream) {
+  switch (nkv * 10 + wpk) {
+    case 81: return rows::launch<8, 1, 3>(p, groups, stream);
+    case 41: return rows::launch<4, 1, 4>(p, groups, stream);
+    case 21: return rows::launch<2, 1, 4>(p, groups, stream);
+    case 42: return rows::launch<4, 2, 4>(p, groups, stream);
+    case 22: return rows::launch<2, 2, 4>(p, groups, stream);
+    default: return fail(SLMT_ERR_INVALID, "paged decode: no whole-row kernel for this shape");
+  }
+}
+
+}  // namespace slmt

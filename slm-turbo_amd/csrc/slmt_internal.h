@@ -73,6 +73,27 @@ __device__ __forceinline__ void swap32(float x, float& a, float& b) {
   b = __builtin_bit_cast(float, r1);
 }
 
+// Two-register forms: permlane16 swaps the odd rows (16 lanes) of a with the
+// even rows of b; permlane32 swaps the upper half-wave of a with the lower
+// half-wave of b.  Afterwards a + b holds, per row, the sum of a pair of rows
+// of one of the two inputs, so two values are folded at once.
+__device__ __forceinline__ void permlane16_swap_pair(float& a, float& b) {
+  auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(unsigned, a), __builtin_bit_cast(unsigned, b),
+                                            false, false);
+  const unsigned r0 = r[0];
+  const unsigned r1 = r[1];
+  a = __builtin_bit_cast(float, r0);
+  b = __builtin_bit_cast(float, r1);
+}
+__device__ __forceinline__ void permlane32_swap_pair(float& a, float& b) {
+  auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, a), __builtin_bit_cast(unsigned, b),
+                                            false, false);
+  const unsigned r0 = r[0];
+  const unsigned r1 = r[1];
+  a = __builtin_bit_cast(float, r0);
+  b = __builtin_bit_cast(float, r1);
+}
+
 // Reductions over the 16 lanes that share (lane & 3): lanes 4p+g, p = 0..15.
 __device__ __forceinline__ float red16_max(float x) {
   x = fmaxf(x, dpp_f<DPP_ROW_ROR4>(x));
@@ -175,12 +196,22 @@ struct AttnPlan {
   int heads_per_group, groups, waves, W, W_ws;
   bool dma;
   size_t lds_bytes;
+  // whole-row kernel (head_dim 128, 4 or 8 query heads per KV head): KV heads
+  // and waves per KV head of a workgroup, head groups
+  bool rows;
+  int rows_nkv, rows_wpk, rows_groups;
 };
 
 // dma_kv > 0 asks for the paged direct-load plan over a cache row of dma_kv
 // KV heads; it is taken when every head group covers whole, 16-byte aligned
 // KV heads and the LDS ring fits.
 int plan_attention(int B, int H, int G, int D, int dma_kv, AttnPlan* plan);
+
+// Whole-row kernel (attention_rows.hip): its shape for a request (false if it
+// does not apply), the workgroups per head group it may use, and its launch.
+bool rows_shape(int H, int G, int D, int cache_kv, int* nkv, int* wpk, int* groups);
+int rows_max_workgroups(int nkv, int wpk, int groups, int cus);
+int launch_attention_rows(int nkv, int wpk, int groups, const AttnParams& p, hipStream_t stream);
 int64_t attention_workspace_bytes(int B, int H, int KV, int D);
 int launch_attention(int mode, int D, AttnParams& p, void* workspace, int64_t ws_bytes,
                      hipStream_t stream);
