@@ -50,32 +50,40 @@ using namespace attn;
 
 constexpr int D = 128, SLOT = D + 8, KD = D / 8;
 
-template <int NKV, int WPK, int NS>
+template <int NKV, int WPK, int NS, int TT>
 struct Shape {
   static_assert(NKV % 2 == 0, "sub-rows must be a whole number of 16-byte units");
+  static_assert(TT % 16 == 0 && NS >= 2 && NS <= 4, "tiles of whole QK rounds, 2-4 ring stages");
   static constexpr int WAVES = NKV * WPK;
   static constexpr int THREADS = WAVES * 64;
   static constexpr int UPR = NKV * SLOT / 16;   // 16-byte units of a sub-row
   static constexpr int RP = UPR | 1;            // units of a staged row
   static constexpr int RSTRIDE = RP * 16;
-  static constexpr int RW = DTILE / WAVES;      // rows copied per wave
-  static_assert(DTILE % WAVES == 0 && RW <= 16, "a wave's rows must lie in one block");
+  static constexpr int RW = TT / WAVES;         // rows copied per wave
+  static_assert(TT % WAVES == 0 && RW <= 16 && 16 % RW == 0, "a wave's rows must lie in one block");
   static constexpr int WUNITS = RW * RP;
   static constexpr int NOPS = (WUNITS + 63) / 64;
   static constexpr int LAST = WUNITS - 64 * (NOPS - 1);   // lanes of the wave's last load
-  static constexpr int STAGE = DTILE * RSTRIDE;
-  static constexpr int QOFF = NS * STAGE;                  // query slots [NS][WAVES] x 1 KB
-  static constexpr int WOFF = QOFF + NS * WAVES * 1024;    // per-wave limb / weight scratch
-  static constexpr int MOFF = WOFF + WAVES * 1024;         // misc ints
+  static constexpr int ROUNDS = TT / 16;                  // QK rounds of 16 tokens
+  static constexpr int NP = TT / 8;                       // PV token pairs per lane
+  static constexpr int STAGE = TT * RSTRIDE;
+  // Query slots: one per ring stage and wave; with a 2-stage ring one per
+  // wave, which the next tile's query load reuses only after begin() read it.
+  static constexpr int QSETS = NS == 2 ? 1 : NS;
+  static constexpr int WSLOT = TT * 8;                    // weight bytes per tile: [pair][head] fp16 x 2
+  static_assert(NS * WSLOT <= 1024, "weight slots must fit the 1 KB scratch");
+  static constexpr int QOFF = NS * STAGE;                 // query slots [QSETS][WAVES] x 1 KB
+  static constexpr int WOFF = QOFF + QSETS * WAVES * 1024; // per-wave limb / weight scratch
+  static constexpr int MOFF = WOFF + WAVES * 1024;        // misc ints
   static constexpr int LDS = MOFF + 32 * 4;
   static_assert(LDS <= 160 * 1024, "LDS ring too large");
 };
 
 constexpr float kC = 1.4426950408889634f / 11.313708498984761f;   // log2(e) / sqrt(128)
 
-template <int NKV, int WPK, int NS>
+template <int NKV, int WPK, int NS, int TT>
 __global__ void __launch_bounds__(NKV * WPK * 64) rows_kernel(const AttnParams p) {
-  using S = Shape<NKV, WPK, NS>;
+  using S = Shape<NKV, WPK, NS, TT>;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
 
   const int tid = threadIdx.x;
@@ -91,13 +99,15 @@ __global__ void __launch_bounds__(NKV * WPK * 64) rows_kernel(const AttnParams p
   uint8_t* const wscr = smem + S::WOFF + wave * 1024;
 
   TileRange rng;
-  if (!schedule_range<DTILE, D>(p, misc, h0, h1, rng)) return;
+  if (!schedule_range<TT, D>(p, misc, h0, h1, rng)) return;
   const int T = rng.T, Weff = rng.Weff, lo = rng.lo, hi = rng.hi;
 
   // ---------------------------------------------------------------- loads
-  // Load i of the wave moves LDS units 64i .. 64i+63 of its run; lane l unit
+  // The wave copies rows rw0 .. rw0+RW-1 of each tile, consecutive rows of one
+  // paged block.  Load i moves LDS units 64i .. 64i+63 of its run; lane l unit
   // u = 64i + l = row rw0 + u / RP, column u % RP (the pad column re-reads
-  // column UPR-1).
+  // column UPR-1), at byte (u / RP) * cache_row + a0 + 16 * column from the
+  // wave's first row.
   const int cache_row = p.cache_kv * SLOT;
   const int a0 = kv_lo * SLOT;
   const int rw0 = wave * S::RW;
@@ -105,8 +115,8 @@ __global__ void __launch_bounds__(NKV * WPK * 64) rows_kernel(const AttnParams p
 #pragma unroll
   for (int i = 0; i < S::NOPS; ++i) {
     const int u = 64 * i + lane;
-    const int r = rw0 + u / S::RP, c = min(u % S::RP, S::UPR - 1);
-    goff[i] = u < S::WUNITS ? (uint32_t)((r & 15) * cache_row + a0 + c * 16) : 0u;
+    const int r = u / S::RP, c = min(u % S::RP, S::UPR - 1);
+    goff[i] = u < S::WUNITS ? (uint32_t)(r * cache_row + a0 + c * 16) : 0u;
   }
   const uint32_t lds_smem = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)smem;
   const uint32_t lds_run = lds_smem + rw0 * S::RSTRIDE;
@@ -114,25 +124,25 @@ __global__ void __launch_bounds__(NKV * WPK * 64) rows_kernel(const AttnParams p
   const int qp = lane >> 2, qg = lane & 3;
   const uint32_t qoff = (uint32_t)(((hw + qg) * p.q_head_stride + qp * 8) * 2);
 
-  // Tile descriptors, 64 tiles at a time, lane i for tile dchunk + i: the base
-  // of this wave's block run and an info word
+  // Tile descriptors, 64 tiles at a time, lane i for tile dchunk + i: the
+  // address of this wave's first row and an info word
   //   sequence << 8 | first tile of the sequence << 7 | last tile << 6 | (valid tokens - 1).
   // Block-table entries are read as their low 32 bits (num_blocks < 2^31).
   const int esh = p.bt64 ? 3 : 2;
   const uint8_t* btab = reinterpret_cast<const uint8_t*>(p.block_tables);
   const int64_t blk_bytes = (int64_t)p.block_size * cache_row;
-  const int hoff = rw0 >= 16 ? 16 : 0;          // the wave's rows are tokens tok0 + hoff ..
+
   uint32_t dlo = 0, dhi = 0;
   int dinfo = 0, dchunk = lo;
   int cb = rng.b, cP = rng.Pb;                  // a sequence at or before the next chunk's first tile
   auto build = [&](int first) {
     int b = cb, P = cP;
-    int L = seq_len_of(p, b), Tb = tiles_of<DTILE>(L);
+    int L = seq_len_of(p, b), Tb = tiles_of<TT>(L);
     while (first >= P + Tb && b + 1 < p.B) {
       P += Tb;
       ++b;
       L = seq_len_of(p, b);
-      Tb = tiles_of<DTILE>(L);
+      Tb = tiles_of<TT>(L);
     }
     cb = b;
     cP = P;
@@ -149,36 +159,56 @@ __global__ void __launch_bounds__(NKV * WPK * 64) rows_kernel(const AttnParams p
       if (!__builtin_amdgcn_ballot_w64(t >= P && t < hi) || b + 1 >= p.B) break;
       ++b;
       L = seq_len_of(p, b);
-      Tb = tiles_of<DTILE>(L);
+      Tb = tiles_of<TT>(L);
     }
     uint64_t base = reinterpret_cast<uint64_t>(p.cache);
     dinfo = 0;
     if (mb >= 0 && t < hi) {
-      const int tok0 = mtb * DTILE;
-      const int tok = tok0 + hoff < mL ? tok0 + hoff : tok0;   // past the end: any valid block
+      const int tok0 = mtb * TT;
+      const int tok = tok0 + rw0 < mL ? tok0 + rw0 : tok0;     // past the end: any valid block
       const int32_t e =
           *reinterpret_cast<const int32_t*>(btab + (((int64_t)mb * p.bt_stride + (tok >> p.block_shift)) << esh));
       base += (uint64_t)(uint32_t)e * (uint64_t)blk_bytes + (uint64_t)((tok & (p.block_size - 1)) * cache_row);
-      dinfo = (mb << 8) | ((mtb == 0) << 7) | ((mtb == mTb - 1) << 6) | (min(DTILE, mL - tok0) - 1);
+      dinfo = (mb << 8) | ((mtb == 0) << 7) | ((mtb == mTb - 1) << 6) | (min(TT, mL - tok0) - 1);
     }
     dlo = (uint32_t)base;
     dhi = (uint32_t)(base >> 32);
     dchunk = first;
   };
-  // Issues tile t into ring stage st; returns its info word.
-  auto issue = [&](int t, int st) -> int {
+  // Tile t's loads into ring stage st, split in parts so that they spread
+  // over the iteration: `fetch` reads the tile's descriptor, `loads` issues
+  // this wave's loads [k0, k1), `qload` the query rows of a sequence start.
+  struct Pending {
+    const uint8_t* base;
+    uint32_t dst;
+    int info, t;
+  };
+  auto fetch = [&](int t, int st) -> Pending {
     const int i = t - dchunk;
-    const uint8_t* base = reinterpret_cast<const uint8_t*>((uint64_t)readlane_u32(dlo, i) |
-                                                           ((uint64_t)readlane_u32(dhi, i) << 32));
-    const int info = __builtin_amdgcn_readlane(dinfo, i);
-    const uint32_t dst = lds_run + st * S::STAGE;
+    Pending d;
+    d.base = reinterpret_cast<const uint8_t*>((uint64_t)readlane_u32(dlo, i) | ((uint64_t)readlane_u32(dhi, i) << 32));
+    d.info = __builtin_amdgcn_readlane(dinfo, i);
+    d.dst = lds_run + st * S::STAGE;
+    d.t = t;
+    return d;
+  };
+  auto loads = [&](const Pending& d, auto k0c, auto k1c) {
+    constexpr int k0 = decltype(k0c)::value, k1 = decltype(k1c)::value;
 #pragma unroll
-    for (int k = 0; k < S::NOPS; ++k) {
-      if (k < S::NOPS - 1 || S::LAST == 64 || lane < S::LAST) lds_load16(base, goff[k], dst + k * 1024);
+    for (int k = k0; k < k1; ++k) {
+      if (k < S::NOPS - 1 || S::LAST == 64 || lane < S::LAST) lds_load16(d.base, goff[k], d.dst + k * 1024);
     }
-    if (((info >> 7) & 1) || t == lo)
-      lds_load16(p.q + (int64_t)(info >> 8) * p.q_seq_stride, qoff, lds_smem + S::QOFF + (st * S::WAVES + wave) * 1024);
-    return info;
+  };
+  auto qload = [&](const Pending& d, int st) {
+    if (((d.info >> 7) & 1) || d.t == lo)
+      lds_load16(p.q + (int64_t)(d.info >> 8) * p.q_seq_stride, qoff,
+                 lds_smem + S::QOFF + ((S::QSETS == 1 ? 0 : st) * S::WAVES + wave) * 1024);
+  };
+  auto issue = [&](int t, int st) -> int {
+    const Pending d = fetch(t, st);
+    loads(d, std::integral_constant<int, 0>{}, std::integral_constant<int, S::NOPS>{});
+    qload(d, st);
+    return d.info;
   };
 
   // ---------------------------------------------------------------- per-wave state
@@ -282,12 +312,17 @@ __global__ void __launch_bounds__(NKV * WPK * 64) rows_kernel(const AttnParams p
     return ((float)iacc * qa) * kstep + kmin * qb;
   };
 
+  // PV token pairs of this lane's group: pairs P = 8m + 2pq and 8m + 2pq + 1,
+  // i.e. tokens 16m + 4pq .. 16m + 4pq + 3, for m = 0 .. TT/16 - 1.
+  auto pair_of = [&](int j) { return 8 * (j >> 1) + 2 * pq + (j & 1); };
+
   // LDS reads of tile data for this lane: its key quarter and rulers of its
-  // two QK tokens, and its 8 V words (PV, used one iteration later).
-  auto read_tile = [&](const uint8_t* Sb, uint32_t (&kq)[2][4], uint2 (&kr)[2], uint32_t (&xv)[8]) {
+  // QK tokens, and its V words (PV, used one iteration later).
+  auto read_tile = [&](const uint8_t* Sb, uint32_t (&kq)[S::ROUNDS][4], uint2 (&kr)[S::ROUNDS],
+                       uint32_t (&xv)[2 * S::NP]) {
     const int sw = (qg & 1) * 8;
 #pragma unroll
-    for (int r = 0; r < 2; ++r) {
+    for (int r = 0; r < S::ROUNDS; ++r) {
       const uint8_t* kb = Sb + (16 * r + qp) * S::RSTRIDE;
       const uint2 k01 = *reinterpret_cast<const uint2*>(kb + 16 * qg + sw);
       const uint2 k23 = *reinterpret_cast<const uint2*>(kb + 16 * qg + 8 - sw);
@@ -299,28 +334,33 @@ __global__ void __launch_bounds__(NKV * WPK * 64) rows_kernel(const AttnParams p
     }
     const uint8_t* vb = Sb + D / 2 + 4 * pc;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int P = (j < 2 ? 2 * pq + j : 8 + 2 * pq + j - 2);   // token pair (2P, 2P+1)
+    for (int j = 0; j < S::NP; ++j) {
+      const int P = pair_of(j);
       xv[2 * j] = *reinterpret_cast<const uint32_t*>(vb + (2 * P) * S::RSTRIDE);
       xv[2 * j + 1] = *reinterpret_cast<const uint32_t*>(vb + (2 * P + 1) * S::RSTRIDE);
     }
   };
 
-  // QK and softmax of one tile; its fp16 weights go to the scratch half `wh`
-  // (256 bytes: dword [pair][head] = (w(2i), w(2i+1))).
-  auto qk_softmax = [&](const uint32_t (&kq)[2][4], const uint2 (&kr)[2], int nvalid, uint8_t* wh) {
-    float s2[2];
-    bool tv[2];
+  // QK and softmax of one tile; its fp16 weights go to the scratch slot `wh`
+  // (dword [pair][head] = (w(2i), w(2i+1))).
+  auto qk_softmax = [&](const uint32_t (&kq)[S::ROUNDS][4], const uint2 (&kr)[S::ROUNDS], int nvalid, uint8_t* wh) {
+    float s2[S::ROUNDS];
+    bool tv[S::ROUNDS];
+    bool any_grow = false;
 #pragma unroll
-    for (int r = 0; r < 2; ++r) {
+    for (int r = 0; r < S::ROUNDS; ++r) {
       tv[r] = 16 * r + qp < nvalid;
       const float sc = score(kq[r], kr[r]);
       s2[r] = tv[r] ? sc : -INFINITY;
+      any_grow = any_grow || s2[r] > m_run;
     }
     // online softmax: the running max per head is only recomputed (and the
     // sums rescaled) when some score of the tile exceeds it
-    if (__builtin_amdgcn_ballot_w64(s2[0] > m_run || s2[1] > m_run)) {
-      const float tmax = red16_max(fmaxf(s2[0], s2[1]));
+    if (__builtin_amdgcn_ballot_w64(any_grow)) {
+      float tl = s2[0];
+#pragma unroll
+      for (int r = 1; r < S::ROUNDS; ++r) tl = fmaxf(tl, s2[r]);
+      const float tmax = red16_max(tl);
       const bool grow = tmax > m_run;
       const float alpha = grow ? __builtin_amdgcn_exp2f(m_run - tmax) : 1.f;   // 0 when growing from -inf
       l_run *= alpha;
@@ -338,7 +378,7 @@ __global__ void __launch_bounds__(NKV * WPK * 64) rows_kernel(const AttnParams p
     }
     uint16_t* w16 = reinterpret_cast<uint16_t*>(wh);
 #pragma unroll
-    for (int r = 0; r < 2; ++r) {
+    for (int r = 0; r < S::ROUNDS; ++r) {
       // m_run > -inf here: token 0 of every tile is valid
       const float pr = __builtin_amdgcn_exp2f(s2[r] - m_run);
       const float vmin = h2f((uint16_t)(kr[r].y & 0xffffu));
@@ -350,12 +390,11 @@ __global__ void __launch_bounds__(NKV * WPK * 64) rows_kernel(const AttnParams p
     }
   };
 
-  // PV of one tile from its V words and the weights in scratch half `wh`.
-  auto pv = [&](const uint32_t (&xv)[8], const uint8_t* wh) {
+  // PV of one tile from its V words and the weights in scratch slot `wh`.
+  auto pv = [&](const uint32_t (&xv)[2 * S::NP], const uint8_t* wh) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int P = (j < 2 ? 2 * pq + j : 8 + 2 * pq + j - 2);
-      const uint4 wq = *reinterpret_cast<const uint4*>(wh + P * 16);
+    for (int j = 0; j < S::NP; ++j) {
+      const uint4 wq = *reinterpret_cast<const uint4*>(wh + pair_of(j) * 16);
       const uint32_t whd[4] = {wq.x, wq.y, wq.z, wq.w};
       const uint32_t x0 = xv[2 * j], x1 = xv[2 * j + 1];
 #pragma unroll
@@ -430,11 +469,11 @@ __global__ void __launch_bounds__(NKV * WPK * 64) rows_kernel(const AttnParams p
       if (npend == 0) {
         pb0 = b;
         pP0 = Pb;
-        pT0 = tiles_of<DTILE>(L);
+        pT0 = tiles_of<TT>(L);
       } else {
         pb1 = b;
         pP1 = Pb;
-        pT1 = tiles_of<DTILE>(L);
+        pT1 = tiles_of<TT>(L);
       }
       ++npend;
     }
@@ -448,8 +487,11 @@ __global__ void __launch_bounds__(NKV * WPK * 64) rows_kernel(const AttnParams p
   // tile deep: iteration t reads tile t's data from LDS, runs PV of tile t-1
   // (V words kept in registers, weights in that tile's scratch slot) while
   // those reads land, then QK and softmax of tile t.  A segment that ends at
-  // tile t-1 is finished right after its PV.  The loop is unrolled by NS, so
-  // stage numbers are constants: tile lo + j uses stage and weight slot j % NS.
+  // tile t-1 is finished right after its PV.  The next tile's loads are
+  // issued in three parts spread over the iteration; its query load comes
+  // after begin() has read this tile's query (with a 2-stage ring the wave has
+  // a single query slot).  The loop is unrolled by NS, so stage numbers are
+  // constants: tile lo + j uses stage and weight slot j % NS.
   build(lo);
   int sinfo[NS];                // info of the tile in each stage
 #pragma unroll
@@ -459,45 +501,60 @@ __global__ void __launch_bounds__(NKV * WPK * 64) rows_kernel(const AttnParams p
     if (lo + j < hi) sinfo[j] = issue(lo + j, j);
   int seg_first = lo;
   bool seg_whole = false;
-  uint32_t xvp[8];              // V words of the previous tile
+  uint32_t xvp[2 * S::NP];      // V words of the previous tile
   int pinfo = 0;                // info of the previous tile
 #pragma unroll
-  for (int i = 0; i < 8; ++i) xvp[i] = 0;
+  for (int i = 0; i < 2 * S::NP; ++i) xvp[i] = 0;
 
   auto iteration = [&](int t, auto stage) {
     constexpr int st = decltype(stage)::value;
     constexpr int sprev = (st + NS - 1) % NS;
+    constexpr int K1 = (S::NOPS + 2) / 3, K2 = (2 * S::NOPS + 2) / 3;
+    using IC0 = std::integral_constant<int, 0>;
+    using IC1 = std::integral_constant<int, K1>;
+    using IC2 = std::integral_constant<int, K2>;
+    using IC3 = std::integral_constant<int, S::NOPS>;
     // tiles t+1 .. t+NS-2 may still be in flight, NOPS loads each (query
     // loads among them only make the bound stricter); near the end of the
     // range fewer follow and the wait is for everything
-    if (t + NS - 2 < hi) vm_wait_n<S::NOPS * (NS - 2)>();
+    if (NS > 2 && t + NS - 2 < hi) vm_wait_n<S::NOPS * (NS - 2)>();
     else vm_wait_n<0>();
     lds_barrier();
     const int info = sinfo[st];
+    const bool first_of_seq = (info >> 7) & 1;
     const int tn = t + NS - 1;
-    if (tn < hi) {
+    const bool more = tn < hi;
+    // tile t+NS-1 goes into the stage tile t-1 used, in three parts; its
+    // query load (into a slot that begin() below may still have to read) last
+    Pending nx;
+    if (more) {
       if (tn - dchunk >= 64) build(tn);
-      sinfo[sprev] = issue(tn, sprev);
+      nx = fetch(tn, sprev);
+      sinfo[sprev] = nx.info;
+      loads(nx, IC0{}, IC1{});
     }
-    uint32_t kq[2][4], xv[8];
-    uint2 kr[2];
+    uint32_t kq[S::ROUNDS][4], xv[2 * S::NP];
+    uint2 kr[S::ROUNDS];
     read_tile(smem + st * S::STAGE + kvw * SLOT, kq, kr, xv);
     if (t > lo) {
-      pv(xvp, wscr + sprev * 256);
+      pv(xvp, wscr + sprev * S::WSLOT);
       if ((pinfo >> 6) & 1) finish(pinfo >> 8, seg_first, seg_whole, true);
     }
-    const bool first_of_seq = (info >> 7) & 1;
+    if (more) loads(nx, IC1{}, IC2{});
     if (t == lo || first_of_seq) {
       seg_first = t;
       seg_whole = first_of_seq;
-      begin(smem + S::QOFF + (st * S::WAVES + wave) * 1024);
+      begin(smem + S::QOFF + ((S::QSETS == 1 ? 0 : st) * S::WAVES + wave) * 1024);
     }
-    qk_softmax(kq, kr, (info & 63) + 1, wscr + st * 256);
+    if (more) {
+      loads(nx, IC2{}, IC3{});
+      qload(nx, sprev);
+    }
+    qk_softmax(kq, kr, (info & 63) + 1, wscr + st * S::WSLOT);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) xvp[i] = xv[i];
+    for (int i = 0; i < 2 * S::NP; ++i) xvp[i] = xv[i];
     pinfo = info;
   };
-  static_assert(NS >= 2 && NS <= 4, "one unrolled step per ring stage");
   for (int t = lo; t < hi; t += NS) {
     iteration(t, std::integral_constant<int, 0>{});
     if (t + 1 < hi) iteration(t + 1, std::integral_constant<int, 1>{});
@@ -507,7 +564,7 @@ __global__ void __launch_bounds__(NKV * WPK * 64) rows_kernel(const AttnParams p
   // the range's last tile: its weights are in this wave's scratch (the wave's
   // own LDS writes are ordered before its reads)
   wave_lds_sync();
-  pv(xvp, wscr + ((hi - 1 - lo) % NS) * 256);
+  pv(xvp, wscr + ((hi - 1 - lo) % NS) * S::WSLOT);
   finish(pinfo >> 8, seg_first, seg_whole, (pinfo >> 6) & 1);
 
   // ---------------------------------------------------------------- arrivals and merges
@@ -545,10 +602,10 @@ static int blocks_per_cu(const void* kern, int threads, size_t lds) {
   return n;
 }
 
-template <int NKV, int WPK, int NS>
+template <int NKV, int WPK, int NS, int TT>
 static int launch(AttnParams p, int groups, hipStream_t stream) {
-  using S = Shape<NKV, WPK, NS>;
-  auto kern = rows_kernel<NKV, WPK, NS>;
+  using S = Shape<NKV, WPK, NS, TT>;
+  auto kern = rows_kernel<NKV, WPK, NS, TT>;
   const int per_cu = blocks_per_cu(reinterpret_cast<const void*>(kern), S::THREADS, S::LDS);
   const int cus = device_cu_count();
   int W = std::max(1, cus * std::max(1, per_cu) / groups);
@@ -578,17 +635,20 @@ bool rows_shape(int H, int G, int D, int cache_kv, int* nkv, int* wpk, int* grou
   return true;
 }
 
+// Instantiations (KV heads per workgroup, waves per KV head, ring stages,
+// tokens per tile): 64-token tiles with a 2-stage ring where a wave's rows
+// fit one 16-row block, 32-token tiles otherwise.
+#define SLMT_ROWS_CONFIGS(X) X(8, 1, 2, 64) X(4, 1, 2, 64) X(2, 1, 4, 32) X(4, 2, 2, 64) X(2, 2, 2, 64)
+
 // Workgroups per head group the whole-row kernel may use (its workspace bound).
 int rows_max_workgroups(int nkv, int wpk, int groups, int cus) {
   const int waves = nkv * wpk;
   // at most 8 waves per CU (up to 256 VGPRs each), and the ring's LDS
   size_t lds = 0;
   switch (nkv * 10 + wpk) {
-    case 81: lds = rows::Shape<8, 1, 3>::LDS; break;
-    case 41: lds = rows::Shape<4, 1, 4>::LDS; break;
-    case 21: lds = rows::Shape<2, 1, 4>::LDS; break;
-    case 42: lds = rows::Shape<4, 2, 4>::LDS; break;
-    case 22: lds = rows::Shape<2, 2, 4>::LDS; break;
+#define SLMT_ROWS_LDS(a, b, c, d) case a * 10 + b: lds = rows::Shape<a, b, c, d>::LDS; break;
+    SLMT_ROWS_CONFIGS(SLMT_ROWS_LDS)
+#undef SLMT_ROWS_LDS
     default: return 1;
   }
   int per_cu = std::min(8 / waves, (int)((160 * 1024) / lds));
@@ -598,11 +658,9 @@ int rows_max_workgroups(int nkv, int wpk, int groups, int cus) {
 
 int launch_attention_rows(int nkv, int wpk, int groups, const AttnParams& p, hipStream_t stream) {
   switch (nkv * 10 + wpk) {
-    case 81: return rows::launch<8, 1, 3>(p, groups, stream);
-    case 41: return rows::launch<4, 1, 4>(p, groups, stream);
-    case 21: return rows::launch<2, 1, 4>(p, groups, stream);
-    case 42: return rows::launch<4, 2, 4>(p, groups, stream);
-    case 22: return rows::launch<2, 2, 4>(p, groups, stream);
+#define SLMT_ROWS_LAUNCH(a, b, c, d) case a * 10 + b: return rows::launch<a, b, c, d>(p, groups, stream);
+    SLMT_ROWS_CONFIGS(SLMT_ROWS_LAUNCH)
+#undef SLMT_ROWS_LAUNCH
     default: return fail(SLMT_ERR_INVALID, "paged decode: no whole-row kernel for this shape");
   }
 }
