@@ -50,10 +50,11 @@ using namespace attn;
 
 constexpr int D = 128, SLOT = D + 8, KD = D / 8;
 
-template <int NKV, int WPK, int NS, int TT>
+template <int NKV, int WPK, int TT>
 struct Shape {
   static_assert(NKV % 2 == 0, "sub-rows must be a whole number of 16-byte units");
-  static_assert(TT % 16 == 0 && NS >= 2 && NS <= 4, "tiles of whole QK rounds, 2-4 ring stages");
+  static_assert(TT % 16 == 0, "tiles of whole QK rounds");
+  static constexpr int NS = 2;                  // LDS ring stages
   static constexpr int WAVES = NKV * WPK;
   static constexpr int THREADS = WAVES * 64;
   static constexpr int UPR = NKV * SLOT / 16;   // 16-byte units of a sub-row
@@ -67,13 +68,10 @@ struct Shape {
   static constexpr int ROUNDS = TT / 16;                  // QK rounds of 16 tokens
   static constexpr int NP = TT / 8;                       // PV token pairs per lane
   static constexpr int STAGE = TT * RSTRIDE;
-  // Query slots: one per ring stage and wave; with a 2-stage ring one per
-  // wave, which the next tile's query load reuses only after begin() read it.
-  static constexpr int QSETS = NS == 2 ? 1 : NS;
   static constexpr int WSLOT = TT * 8;                    // weight bytes per tile: [pair][head] fp16 x 2
   static_assert(NS * WSLOT <= 1024, "weight slots must fit the 1 KB scratch");
-  static constexpr int QOFF = NS * STAGE;                 // query slots [QSETS][WAVES] x 1 KB
-  static constexpr int WOFF = QOFF + QSETS * WAVES * 1024; // per-wave limb / weight scratch
+  static constexpr int QOFF = NS * STAGE;                 // one 1 KB query slot per wave
+  static constexpr int WOFF = QOFF + WAVES * 1024;        // per-wave limb / weight scratch
   static constexpr int MOFF = WOFF + WAVES * 1024;        // misc ints
   static constexpr int LDS = MOFF + 32 * 4;
   static_assert(LDS <= 160 * 1024, "LDS ring too large");
@@ -81,9 +79,9 @@ struct Shape {
 
 constexpr float kC = 1.4426950408889634f / 11.313708498984761f;   // log2(e) / sqrt(128)
 
-template <int NKV, int WPK, int NS, int TT>
+template <int NKV, int WPK, int TT>
 __global__ void __launch_bounds__(NKV * WPK * 64) rows_kernel(const AttnParams p) {
-  using S = Shape<NKV, WPK, NS, TT>;
+  using S = Shape<NKV, WPK, TT>;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
 
   const int tid = threadIdx.x;
@@ -175,13 +173,12 @@ __global__ void __launch_bounds__(NKV * WPK * 64) rows_kernel(const AttnParams p
     dhi = (uint32_t)(base >> 32);
     dchunk = first;
   };
-  // Tile t's loads into ring stage st, split in parts so that they spread
-  // over the iteration: `fetch` reads the tile's descriptor, `loads` issues
-  // this wave's loads [k0, k1), `qload` the query rows of a sequence start.
+  // Tile t's rows into ring stage st, in parts: `fetch` reads the tile's
+  // descriptor, `loads` issues this wave's loads [k0, k1).
   struct Pending {
     const uint8_t* base;
     uint32_t dst;
-    int info, t;
+    int info;
   };
   auto fetch = [&](int t, int st) -> Pending {
     const int i = t - dchunk;
@@ -189,7 +186,6 @@ __global__ void __launch_bounds__(NKV * WPK * 64) rows_kernel(const AttnParams p
     d.base = reinterpret_cast<const uint8_t*>((uint64_t)readlane_u32(dlo, i) | ((uint64_t)readlane_u32(dhi, i) << 32));
     d.info = __builtin_amdgcn_readlane(dinfo, i);
     d.dst = lds_run + st * S::STAGE;
-    d.t = t;
     return d;
   };
   auto loads = [&](const Pending& d, auto k0c, auto k1c) {
@@ -199,28 +195,27 @@ __global__ void __launch_bounds__(NKV * WPK * 64) rows_kernel(const AttnParams p
       if (k < S::NOPS - 1 || S::LAST == 64 || lane < S::LAST) lds_load16(d.base, goff[k], d.dst + k * 1024);
     }
   };
-  auto qload = [&](const Pending& d, int st) {
-    if (((d.info >> 7) & 1) || d.t == lo)
-      lds_load16(p.q + (int64_t)(d.info >> 8) * p.q_seq_stride, qoff,
-                 lds_smem + S::QOFF + ((S::QSETS == 1 ? 0 : st) * S::WAVES + wave) * 1024);
-  };
   auto issue = [&](int t, int st) -> int {
     const Pending d = fetch(t, st);
     loads(d, std::integral_constant<int, 0>{}, std::integral_constant<int, S::NOPS>{});
-    qload(d, st);
     return d.info;
   };
+  // Issues the query rows of sequence b into this wave's query slot.
+  const uint32_t qslot = lds_smem + S::QOFF + wave * 1024;
+  auto issue_q = [&](int b) { lds_load16(p.q + (int64_t)b * p.q_seq_stride, qoff, qslot); };
 
   // ---------------------------------------------------------------- per-wave state
   // QK lane (token p, key quarter qc = lane & 3): limbs of all 4 heads for
   // the lane's 4 key dwords, in the order the lane reads them (odd quarters
-  // read their two 8-byte halves swapped, so the quad covers all 32 banks)
-  uint32_t qlq[4][4][4];              // [head][dword][limb]
+  // read their two 8-byte halves swapped, so the quad covers all 32 banks).
+  // Heads are stored rotated: slot j holds head (qc + j) & 3, so the quad's
+  // reduce-scatter needs no per-lane selects.
+  uint32_t qlq[4][4][4];              // [head slot][dword][limb]
   float qa = 0.f, qb = 0.f, m_run = -INFINITY, l_run = 0.f, vmt = 0.f;
   float accl[4][4], accf[4][4];       // [byte k][head]: sum w * lo, sum w * (lo + 16 hi), units of 2^-24
   const int pc = lane & 15, pq = lane >> 4;   // PV: dword column, token group
 
-  auto begin = [&](const uint8_t* qlds) {
+  auto begin = [&](const uint4 w) {
     m_run = -INFINITY;
     l_run = 0.f;
     vmt = 0.f;
@@ -228,7 +223,6 @@ __global__ void __launch_bounds__(NKV * WPK * 64) rows_kernel(const AttnParams p
     for (int k = 0; k < 4; ++k)
 #pragma unroll
       for (int h = 0; h < 4; ++h) accl[k][h] = accf[k][h] = 0.f;
-    const uint4 w = *reinterpret_cast<const uint4*>(qlds + lane * 16);
     const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
     float qv[8];
 #pragma unroll
@@ -265,47 +259,53 @@ __global__ void __launch_bounds__(NKV * WPK * 64) rows_kernel(const AttnParams p
     // (head h, limb k) words 4qc .. 4qc+3 of this lane's quarter
     const bool swp = qg & 1;
 #pragma unroll
-    for (int h = 0; h < 4; ++h)
+    for (int j = 0; j < 4; ++j)
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
+        const int h = (qg + j) & 3;
         const uint4 v = *reinterpret_cast<const uint4*>(wl + (h * 4 + k) * 16 + 4 * qg);
-        qlq[h][0][k] = swp ? v.z : v.x;
-        qlq[h][1][k] = swp ? v.w : v.y;
-        qlq[h][2][k] = swp ? v.x : v.z;
-        qlq[h][3][k] = swp ? v.y : v.w;
+        qlq[j][0][k] = swp ? v.z : v.x;
+        qlq[j][1][k] = swp ? v.w : v.y;
+        qlq[j][2][k] = swp ? v.x : v.z;
+        qlq[j][3][k] = swp ? v.y : v.w;
       }
     qa = kC * rsq;
     qb = kC * qsum;
   };
 
   // Score of this lane's token for head qg (base-2 units): the lane's key
-  // quarter kq against all 4 heads' limbs, the quad's partial dots added by a
-  // reduce-scatter that leaves head c's sum in lane c; kr: the token's rulers.
+  // quarter kq against all 4 heads' limbs (Horner over the limbs: the dot8
+  // accumulator is shifted by 4 bits between limbs), then the quad's partial
+  // dots for head qg gathered from the rotated slots with three DPP adds;
+  // kr: the token's rulers.
   auto score = [&](const uint32_t (&kq)[4], uint2 kr) -> float {
-    uint32_t a[4][4];
-#pragma unroll
-    for (int h = 0; h < 4; ++h)
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        uint32_t x = 0;
-#pragma unroll
-        for (int d = 0; d < 4; ++d) x = __builtin_amdgcn_udot8(kq[d], qlq[h][d][k], x, false);
-        a[h][k] = x;
-      }
     uint32_t part[4];
 #pragma unroll
-    for (int h = 0; h < 4; ++h) part[h] = a[h][0] + (a[h][1] << 4) + (a[h][2] << 8) + (a[h][3] << 12);
+    for (int j = 0; j < 4; ++j) {
+      uint32_t x = 0;
+#pragma unroll
+      for (int k = 3; k >= 0; --k) {
+        if (k < 3) x <<= 4;
+#pragma unroll
+        for (int d = 0; d < 4; ++d) x = __builtin_amdgcn_udot8(kq[d], qlq[j][d][k], x, false);
+      }
+      part[j] = x;
+    }
     // nibble sum of the token: the quad's quarters
     uint32_t sn = 0;
 #pragma unroll
     for (int d = 0; d < 4; ++d) sn = __builtin_amdgcn_udot8(kq[d], 0x11111111u, sn, false);
+    // (the empty asm keeps each DPP move next to a two-operand add, which the
+    // backend then fuses into one v_add_u32_dpp)
     sn += dpp_u<DPP_QUAD_XOR1>(sn);
+    asm volatile("" : "+v"(sn));
     sn += dpp_u<DPP_QUAD_XOR2>(sn);
-    // reduce-scatter over the quad: lane c ends with head c
-    const bool o1 = qg & 1, o2 = qg & 2;
-    const uint32_t ya = (o1 ? part[1] : part[0]) + dpp_u<DPP_QUAD_XOR1>(o1 ? part[0] : part[1]);
-    const uint32_t yb = (o1 ? part[3] : part[2]) + dpp_u<DPP_QUAD_XOR1>(o1 ? part[2] : part[3]);
-    const uint32_t z = (o2 ? yb : ya) + dpp_u<DPP_QUAD_XOR2>(o2 ? ya : yb);
+    // lane c: head c lives in slot 0 here, slot 3 of lane c+1, 2 of c+2, 1 of c+3
+    uint32_t z = part[0] + dpp_u<DPP_QUAD_ROT1>(part[3]);
+    asm volatile("" : "+v"(z));
+    z += dpp_u<DPP_QUAD_XOR2>(part[2]);
+    asm volatile("" : "+v"(z));
+    z += dpp_u<DPP_QUAD_ROT3>(part[1]);
     const int iacc = (int)z - (int)(sn << 15);
     const float kmin = h2f((uint16_t)(kr.x & 0xffffu));
     const float kstep = h2f((uint16_t)(kr.x >> 16));
@@ -480,25 +480,24 @@ __global__ void __launch_bounds__(NKV * WPK * 64) rows_kernel(const AttnParams p
   };
 
   // ---------------------------------------------------------------- pipeline
-  // Tiles lo .. lo+NS-2 are issued up front; iteration t waits for this
-  // wave's loads of tile t, meets the other waves at a barrier (tile t is then
-  // complete in LDS and every wave is done with tile t-1), and issues tile
-  // t+NS-1 into the stage tile t-1 used.  Compute is software-pipelined one
-  // tile deep: iteration t reads tile t's data from LDS, runs PV of tile t-1
-  // (V words kept in registers, weights in that tile's scratch slot) while
-  // those reads land, then QK and softmax of tile t.  A segment that ends at
-  // tile t-1 is finished right after its PV.  The next tile's loads are
-  // issued in three parts spread over the iteration; its query load comes
-  // after begin() has read this tile's query (with a 2-stage ring the wave has
-  // a single query slot).  The loop is unrolled by NS, so stage numbers are
-  // constants: tile lo + j uses stage and weight slot j % NS.
+  // Two LDS stages; tile t lives in stage (t - lo) & 1 and is issued two
+  // iterations ahead.  Iteration t:
+  //   wait for this wave's loads of tile t (tile t+1's may still fly), then a
+  //   barrier: tile t is complete in LDS;
+  //   read all of tile t this lane needs into registers (and the segment's
+  //   query rows), run PV of tile t-1 from registers while the reads land,
+  //   finish a segment that ended at tile t-1;
+  //   a second barrier: every wave is done reading the stage, which now takes
+  //   tile t+2 (after the query rows of tile t+1 when that starts a segment);
+  //   QK and softmax of tile t.
+  // While tile t is computed, tiles t+1 and t+2 are in flight.  The loads of
+  // one tile are followed by at most the next tile's query load and loads,
+  // so waiting until NOPS operations remain covers tile t and its query.
   build(lo);
-  int sinfo[NS];                // info of the tile in each stage
-#pragma unroll
-  for (int j = 0; j < NS; ++j) sinfo[j] = 0;
-#pragma unroll
-  for (int j = 0; j < NS - 1; ++j)
-    if (lo + j < hi) sinfo[j] = issue(lo + j, j);
+  int sinfo[2];
+  sinfo[0] = issue(lo, 0);
+  issue_q(sinfo[0] >> 8);
+  sinfo[1] = lo + 1 < hi ? issue(lo + 1, 1) : 0;
   int seg_first = lo;
   bool seg_whole = false;
   uint32_t xvp[2 * S::NP];      // V words of the previous tile
@@ -508,63 +507,59 @@ __global__ void __launch_bounds__(NKV * WPK * 64) rows_kernel(const AttnParams p
 
   auto iteration = [&](int t, auto stage) {
     constexpr int st = decltype(stage)::value;
-    constexpr int sprev = (st + NS - 1) % NS;
+    constexpr int so = st ^ 1;
+    if (t + 1 < hi) vm_wait_n<S::NOPS>();
+    else vm_wait_n<0>();
+    lds_barrier();
+    const int info = sinfo[st];
+    const bool first_of_seq = (info >> 7) & 1;
+    const bool seg_start = t == lo || first_of_seq;
+    uint32_t kq[S::ROUNDS][4], xv[2 * S::NP];
+    uint2 kr[S::ROUNDS];
+    read_tile(smem + st * S::STAGE + kvw * SLOT, kq, kr, xv);
+    uint4 qw = make_uint4(0u, 0u, 0u, 0u);
+    if (seg_start) qw = *reinterpret_cast<const uint4*>(smem + S::QOFF + wave * 1024 + lane * 16);
+    if (t > lo) {
+      pv(xvp, wscr + so * S::WSLOT);
+      if ((pinfo >> 6) & 1) finish(pinfo >> 8, seg_first, seg_whole, true);
+    }
+    lds_barrier();
+    // tile t+2 into this stage, in three parts spread over the rest of the
+    // iteration
     constexpr int K1 = (S::NOPS + 2) / 3, K2 = (2 * S::NOPS + 2) / 3;
     using IC0 = std::integral_constant<int, 0>;
     using IC1 = std::integral_constant<int, K1>;
     using IC2 = std::integral_constant<int, K2>;
     using IC3 = std::integral_constant<int, S::NOPS>;
-    // tiles t+1 .. t+NS-2 may still be in flight, NOPS loads each (query
-    // loads among them only make the bound stricter); near the end of the
-    // range fewer follow and the wait is for everything
-    if (NS > 2 && t + NS - 2 < hi) vm_wait_n<S::NOPS * (NS - 2)>();
-    else vm_wait_n<0>();
-    lds_barrier();
-    const int info = sinfo[st];
-    const bool first_of_seq = (info >> 7) & 1;
-    const int tn = t + NS - 1;
-    const bool more = tn < hi;
-    // tile t+NS-1 goes into the stage tile t-1 used, in three parts; its
-    // query load (into a slot that begin() below may still have to read) last
+    if (t + 1 < hi && ((sinfo[so] >> 7) & 1)) issue_q(sinfo[so] >> 8);
+    const bool more = t + 2 < hi;
     Pending nx;
     if (more) {
-      if (tn - dchunk >= 64) build(tn);
-      nx = fetch(tn, sprev);
-      sinfo[sprev] = nx.info;
+      if (t + 2 - dchunk >= 64) build(t + 2);
+      nx = fetch(t + 2, st);
+      sinfo[st] = nx.info;
       loads(nx, IC0{}, IC1{});
     }
-    uint32_t kq[S::ROUNDS][4], xv[2 * S::NP];
-    uint2 kr[S::ROUNDS];
-    read_tile(smem + st * S::STAGE + kvw * SLOT, kq, kr, xv);
-    if (t > lo) {
-      pv(xvp, wscr + sprev * S::WSLOT);
-      if ((pinfo >> 6) & 1) finish(pinfo >> 8, seg_first, seg_whole, true);
-    }
-    if (more) loads(nx, IC1{}, IC2{});
-    if (t == lo || first_of_seq) {
+    if (seg_start) {
       seg_first = t;
       seg_whole = first_of_seq;
-      begin(smem + S::QOFF + ((S::QSETS == 1 ? 0 : st) * S::WAVES + wave) * 1024);
+      begin(qw);
     }
-    if (more) {
-      loads(nx, IC2{}, IC3{});
-      qload(nx, sprev);
-    }
+    if (more) loads(nx, IC1{}, IC2{});
     qk_softmax(kq, kr, (info & 63) + 1, wscr + st * S::WSLOT);
+    if (more) loads(nx, IC2{}, IC3{});
 #pragma unroll
     for (int i = 0; i < 2 * S::NP; ++i) xvp[i] = xv[i];
     pinfo = info;
   };
-  for (int t = lo; t < hi; t += NS) {
+  for (int t = lo; t < hi; t += 2) {
     iteration(t, std::integral_constant<int, 0>{});
     if (t + 1 < hi) iteration(t + 1, std::integral_constant<int, 1>{});
-    if constexpr (NS > 2) { if (t + 2 < hi) iteration(t + 2, std::integral_constant<int, 2 % NS>{}); }
-    if constexpr (NS > 3) { if (t + 3 < hi) iteration(t + 3, std::integral_constant<int, 3 % NS>{}); }
   }
   // the range's last tile: its weights are in this wave's scratch (the wave's
   // own LDS writes are ordered before its reads)
   wave_lds_sync();
-  pv(xvp, wscr + ((hi - 1 - lo) % NS) * S::WSLOT);
+  pv(xvp, wscr + ((hi - 1 - lo) & 1) * S::WSLOT);
   finish(pinfo >> 8, seg_first, seg_whole, (pinfo >> 6) & 1);
 
   // ---------------------------------------------------------------- arrivals and merges
@@ -602,10 +597,10 @@ static int blocks_per_cu(const void* kern, int threads, size_t lds) {
   return n;
 }
 
-template <int NKV, int WPK, int NS, int TT>
+template <int NKV, int WPK, int TT>
 static int launch(AttnParams p, int groups, hipStream_t stream) {
-  using S = Shape<NKV, WPK, NS, TT>;
-  auto kern = rows_kernel<NKV, WPK, NS, TT>;
+  using S = Shape<NKV, WPK, TT>;
+  auto kern = rows_kernel<NKV, WPK, TT>;
   const int per_cu = blocks_per_cu(reinterpret_cast<const void*>(kern), S::THREADS, S::LDS);
   const int cus = device_cu_count();
   int W = std::max(1, cus * std::max(1, per_cu) / groups);
@@ -635,10 +630,10 @@ bool rows_shape(int H, int G, int D, int cache_kv, int* nkv, int* wpk, int* grou
   return true;
 }
 
-// Instantiations (KV heads per workgroup, waves per KV head, ring stages,
-// tokens per tile): 64-token tiles with a 2-stage ring where a wave's rows
-// fit one 16-row block, 32-token tiles otherwise.
-#define SLMT_ROWS_CONFIGS(X) X(8, 1, 2, 64) X(4, 1, 2, 64) X(2, 1, 4, 32) X(4, 2, 2, 64) X(2, 2, 2, 64)
+// Instantiations (KV heads per workgroup, waves per KV head, tokens per
+// tile): 64-token tiles where a wave's rows fit one 16-row block, 32-token
+// tiles otherwise.
+#define SLMT_ROWS_CONFIGS(X) X(8, 1, 64) X(4, 1, 64) X(2, 1, 32) X(4, 2, 64) X(2, 2, 64)
 
 // Workgroups per head group the whole-row kernel may use (its workspace bound).
 int rows_max_workgroups(int nkv, int wpk, int groups, int cus) {
@@ -646,7 +641,7 @@ int rows_max_workgroups(int nkv, int wpk, int groups, int cus) {
   // at most 8 waves per CU (up to 256 VGPRs each), and the ring's LDS
   size_t lds = 0;
   switch (nkv * 10 + wpk) {
-#define SLMT_ROWS_LDS(a, b, c, d) case a * 10 + b: lds = rows::Shape<a, b, c, d>::LDS; break;
+#define SLMT_ROWS_LDS(a, b, c) case a * 10 + b: lds = rows::Shape<a, b, c>::LDS; break;
     SLMT_ROWS_CONFIGS(SLMT_ROWS_LDS)
 #undef SLMT_ROWS_LDS
     default: return 1;
@@ -658,7 +653,7 @@ int rows_max_workgroups(int nkv, int wpk, int groups, int cus) {
 
 int launch_attention_rows(int nkv, int wpk, int groups, const AttnParams& p, hipStream_t stream) {
   switch (nkv * 10 + wpk) {
-#define SLMT_ROWS_LAUNCH(a, b, c, d) case a * 10 + b: return rows::launch<a, b, c, d>(p, groups, stream);
+#define SLMT_ROWS_LAUNCH(a, b, c) case a * 10 + b: return rows::launch<a, b, c>(p, groups, stream);
     SLMT_ROWS_CONFIGS(SLMT_ROWS_LAUNCH)
 #undef SLMT_ROWS_LAUNCH
     default: return fail(SLMT_ERR_INVALID, "paged decode: no whole-row kernel for this shape");

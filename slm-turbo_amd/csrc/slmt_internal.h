@@ -37,18 +37,22 @@ __device__ __forceinline__ uint16_t f2h(float f) {  // round to nearest even
 enum : int {
   DPP_QUAD_XOR1 = 0xB1,   // quad_perm [1,0,3,2]
   DPP_QUAD_XOR2 = 0x4E,   // quad_perm [2,3,0,1]
+  DPP_QUAD_ROT1 = 0x39,   // quad_perm [1,2,3,0]: lane i reads lane (i+1) & 3 of its quad
+  DPP_QUAD_ROT3 = 0x93,   // quad_perm [3,0,1,2]: lane i reads lane (i+3) & 3
   DPP_ROW_ROR4 = 0x124,
   DPP_ROW_ROR8 = 0x128,
 };
 
+// Every control used here (quad permutations, rotations within a row) reads
+// a lane of the same row, so no lane keeps its old value: the move has no
+// "old" operand, which lets the backend fuse it into the consuming VALU op.
 template <int CTRL>
 __device__ __forceinline__ uint32_t dpp_u(uint32_t x) {
-  return __builtin_amdgcn_update_dpp(0u, x, CTRL, 0xf, 0xf, false);
+  return (uint32_t)__builtin_amdgcn_mov_dpp((int)x, CTRL, 0xf, 0xf, true);
 }
 template <int CTRL>
 __device__ __forceinline__ float dpp_f(float x) {
-  return __builtin_bit_cast(
-      float, __builtin_amdgcn_update_dpp(0u, __builtin_bit_cast(unsigned, x), CTRL, 0xf, 0xf, false));
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), CTRL, 0xf, 0xf, true));
 }
 
 // Exchange with the partner row (rows 0<->1, 2<->3) and the partner half-wave.
