@@ -5,36 +5,38 @@
 //
 // A workgroup owns NKV consecutive KV heads (a 16-byte aligned sub-row of every
 // cache row, NKV * 136 bytes) and their 4*WPK query heads each, one wave per 4
-// query heads.  Tiles are 32 tokens = 32 sub-rows, two contiguous runs of one
-// paged block each.  Work is split stream-K over the concatenated tile list
-// of all sequences, exactly as in attention_kernel.h, and split sequences are
-// merged by the last workgroup to finish a piece.
+// query heads.  Tiles are TT tokens (64, or 32 where a wave's share of a
+// 64-token tile would cross a paged block).  Work is split stream-K over the
+// concatenated tile list of all sequences, exactly as in attention_kernel.h,
+// and split sequences are merged by the last workgroup to finish a piece.
 //
 // Staging: the workgroup copies each tile with 16-byte direct loads
-// (global_load_lds_dwordx4, no VGPRs) into an LDS ring of NS stages, NS-1
-// tiles ahead; wave w copies rows 32w/W .. 32(w+1)/W, which lie in one paged
-// block.  Every lane chooses its source unit, so the staged rows get an odd
-// number of 16-byte units (the pad unit re-reads the row's last unit): the
-// 16 rows that the QK lanes read at once then fall in 16 different bank
-// groups.  One barrier per tile publishes the stage.
+// (global_load_lds_dwordx4, no VGPRs) into a 2-stage LDS ring, two tiles
+// ahead of the one being computed; wave w copies the TT/WAVES consecutive rows
+// starting at row w*TT/WAVES, which lie in one paged block.  Every lane chooses
+// its source unit, so the staged rows get an odd number of 16-byte units (the
+// pad unit re-reads the row's last unit): the 16 rows that the QK lanes read
+// at once then fall in 16 different bank groups.  Two barriers per tile: one
+// publishes the stage, one releases it for the tile after next.
 //
-// QK (lane = token p of 16 x key quarter c of 4; two rounds per tile): the
+// QK (lane = token p of 16 x key quarter c of 4; TT/16 rounds per tile): the
 // query is quantized once per sequence to 16-bit fixed point and split into
 // four 4-bit limbs; v_dot8_u32_u4 multiplies 8 packed key nibbles by 8 limb
 // nibbles, so keys are never unpacked.  Each lane dots its quarter of the
 // key with all 4 heads; a reduce-scatter over the quad leaves head c's dot in
 // lane c.  q.K = step * q.n + min * sum(q).
 //
-// PV (lane = V dword column c of 16 x token group q of 4): group q takes the
-// token pairs (4q, 4q+1), (4q+2, 4q+3), (16+4q, 17+4q), (18+4q, 19+4q): its
-// rows are 4 apart from the other groups', which with 69-unit rows puts the
-// 4 groups' reads in disjoint banks.  Two tokens' bytes k are packed into one
-// dword (one v_perm_b32) and read as an fp16 pair of subnormals,
-// (lo + 16 hi) * 2^-24, which v_dot2c_f32_f16 multiplies exactly with the fp16
-// weights p * step; a second product with the low nibbles alone (one AND)
-// separates the two dims.  The per-token min enters once per token as
-// sum(p * min).  The 4 groups' partial sums are added at the end of a
-// segment.
+// PV (lane = V dword column c of 16 x token group g of 4): group g takes the
+// tokens 16m + 4g .. 16m + 4g + 3 of each 16-token round m.  The groups' rows
+// are 4 apart, and 4 rows of an odd number of units are 16 banks apart, so
+// each half-wave's two groups read disjoint banks.  Two tokens' bytes k are
+// packed into one dword (one v_perm_b32) and read as an fp16 pair of
+// subnormals, (lo + 16 hi) * 2^-24, which v_dot2c_f32_f16 multiplies exactly
+// with the fp16 weights p * step; a second product with the low nibbles alone
+// (one AND) separates the two dims.  The per-token min enters once per token
+// as sum(p * min).  The 4 groups' partial sums are added at the end of a
+// segment.  PV of a tile runs one iteration after its QK, from V words read
+// into registers with the tile's keys.
 #include "attention_kernel.h"
 
 #include <algorithm>

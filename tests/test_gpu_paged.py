@@ -107,7 +107,11 @@ def _run_batched(case: PagedCase, out_dtype=torch.float32, bt_dtype=torch.int32)
 
 
 @pytest.mark.parametrize("H,KV,D", [(32, 8, 128), (4, 4, 64), (12, 2, 128), (14, 2, 64), (8, 8, 80),
-                                    (16, 8, 64), (64, 8, 128), (32, 4, 128)])
+                                    (16, 8, 64), (64, 8, 128), (32, 4, 128),
+                                    # whole-row kernel: 4 KV heads x 1 wave, 2 KV heads x 2 waves,
+                                    # several head groups per launch; odd KV falls back
+                                    (16, 4, 128), (16, 2, 128), (24, 6, 128), (48, 6, 128), (64, 16, 128),
+                                    (12, 3, 128)])
 def test_paged_batched_matches_oracle(H, KV, D):
     case = make_paged_case(seed=H * 131 + D, B=5, H=H, KV=KV, D=D, len_range=(1, 700))
     assert_close(_run_batched(case), paged_reference(case), what=f"H={H} KV={KV} D={D}")
