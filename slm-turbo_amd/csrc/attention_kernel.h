@@ -239,7 +239,27 @@ struct TileRange {
   int b, Pb;             // sequence holding tile lo and its first global tile
 };
 
-template <int TT, int D>
+// Writes zeros for the sequences of length 0 that workgroup blockIdx.x owns
+// (every Weff-th sequence), heads [h0, h1).
+template <int D>
+__device__ void zero_empty(const AttnParams& p, int h0, int h1, int Weff) {
+  const int tid = threadIdx.x, NT = blockDim.x;
+  for (int b = blockIdx.x; b < p.B; b += Weff) {
+    if (seq_len_of(p, b) == 0) {
+      for (int e = tid; e < (h1 - h0) * D; e += NT) {
+        const int h = h0 + e / D, d = e % D;
+        const int64_t o = (int64_t)b * p.out_seq_stride + (int64_t)h * p.out_head_stride + d;
+        if (p.out_f16) reinterpret_cast<uint16_t*>(p.out)[o] = 0;
+        else reinterpret_cast<float*>(p.out)[o] = 0.0f;
+      }
+    }
+  }
+}
+
+// ZERO: zero the empty sequences' outputs here; otherwise the caller calls
+// zero_empty itself once it has a range (always done here when no workgroup
+// has tiles).
+template <int TT, int D, bool ZERO = true>
 __device__ bool schedule_range(const AttnParams& p, int* misc, int h0, int h1, TileRange& r) {
   const int tid = threadIdx.x, lane = tid & 63, wave = uniform(tid >> 6);
   const int NT = blockDim.x, nwaves = NT >> 6;
@@ -273,16 +293,7 @@ __device__ bool schedule_range(const AttnParams& p, int* misc, int h0, int h1, T
   r.Weff = max(1, min(p.W, (r.T + p.min_tiles - 1) / p.min_tiles));
   const int wg = blockIdx.x;
   if (wg >= r.Weff) return false;
-  for (int b = wg; b < p.B; b += r.Weff) {
-    if (seq_len_of(p, b) == 0) {
-      for (int e = tid; e < (h1 - h0) * D; e += NT) {
-        const int h = h0 + e / D, d = e % D;
-        const int64_t o = (int64_t)b * p.out_seq_stride + (int64_t)h * p.out_head_stride + d;
-        if (p.out_f16) reinterpret_cast<uint16_t*>(p.out)[o] = 0;
-        else reinterpret_cast<float*>(p.out)[o] = 0.0f;
-      }
-    }
-  }
+  if (ZERO || r.T == 0) zero_empty<D>(p, h0, h1, r.Weff);
   if (r.T == 0) return false;
   r.lo = range_start(wg, r.T, r.Weff);
   r.hi = range_start(wg + 1, r.T, r.Weff);
@@ -306,54 +317,96 @@ __device__ bool schedule_range(const AttnParams& p, int* misc, int h0, int h1, T
 }
 
 // Last-arriver merge of sequence b (tiles [Pb, Pb + Tb) of T over Weff
-// workgroups): combines the (m, l, o) partials of every piece, in one pass
-// with a running maximum, and writes the output of heads [h0, h1).  Pieces
-// are read agent-coherently after the arrival counter showed that all of
-// them were published.  For the per-channel layout the V scale/zero are
-// applied to the merged average.
+// workgroups): combines the (m, l, o) partials of every piece and writes the
+// output of heads [h0, h1).  Pieces are read agent-coherently (past this
+// XCD's L2) after the arrival counter showed that all of them were
+// published.  A work item is one pair of dims, consecutive items on
+// consecutive lanes (each load instruction reads whole 64-byte lines); a
+// thread merges IPT items at once, MB pieces per batch, with all of a batch's
+// loads issued together, and updates the running maximum once per batch.  For
+// the per-channel layout the V scale/zero are applied to the merged average.
 template <int D, int MODE>
 __device__ void merge_sequence(const AttnParams& p, int b, int Pb, int Tb, int T, int Weff, int h0, int h1,
                                int group) {
+  static_assert(D % 2 == 0, "work items of 2 dims");
+  constexpr int MB = 4, IPT = 4;
   const int tid = threadIdx.x, NT = blockDim.x, G = p.G;
   const int w_first = range_owner(Pb, T, Weff);
   const int w_last = range_owner(Pb + Tb - 1, T, Weff);
   const int first_slot = (range_start(w_first, T, Weff) == Pb) ? 0 : 1;
-  // 4 consecutive dims per work item
-  for (int e = tid; e < (h1 - h0) * (D / 4); e += NT) {
-    const int h = h0 + e / (D / 4), d = (e - (e / (D / 4)) * (D / 4)) * 4;
-    float M = -INFINITY, Lsum = 0.f;
-    float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll 2
-    for (int w = w_first; w <= w_last; ++w) {
-      const int s = (w == w_first) ? first_slot : 0;
-      const int64_t base = ((int64_t)w * 2 + s) * p.H + h;
-      const float2 ml = load_pair_agent(p.part_ml + base * 2);
-      const float2 o01 = load_pair_agent(p.part_o + base * D + d);
-      const float2 o23 = load_pair_agent(p.part_o + base * D + d + 2);
-      const float Mn = fmaxf(M, ml.x);
-      const float a = __builtin_amdgcn_exp2f(M - Mn);        // 0 for the first piece (M = -inf)
-      const float sc = __builtin_amdgcn_exp2f(ml.x - Mn);
-      Lsum = Lsum * a + sc * ml.y;
-      O.x = O.x * a + sc * o01.x;
-      O.y = O.y * a + sc * o01.y;
-      O.z = O.z * a + sc * o23.x;
-      O.w = O.w * a + sc * o23.y;
-      M = Mn;
-    }
-    const float rL = __builtin_amdgcn_rcpf(Lsum);
-    float r[4] = {O.x * rL, O.y * rL, O.z * rL, O.w * rL};
-    if constexpr (MODE == SRC_CHANNEL) {
-      if (p.use_quant) {
-        const int64_t kvg = h / G;
+  const int total = (h1 - h0) * (D / 2);
+  for (int e0 = tid; e0 < total; e0 += NT * IPT) {
+    int hh[IPT], dd[IPT];
+    float M[IPT], Lsum[IPT];
+    float2 O[IPT];
 #pragma unroll
-        for (int k = 0; k < 4; ++k) r[k] = h2f(p.vr0[kvg * D + d + k]) * (r[k] - h2f(p.vr1[kvg * D + d + k]));
+    for (int k = 0; k < IPT; ++k) {
+      const int e = min(e0 + k * NT, total - 1);   // past the end: a repeat of the last item, not written
+      hh[k] = h0 + e / (D / 2);
+      dd[k] = (e - (e / (D / 2)) * (D / 2)) * 2;
+      M[k] = -INFINITY;
+      Lsum[k] = 0.f;
+      O[k] = make_float2(0.f, 0.f);
+    }
+    for (int w0 = w_first; w0 <= w_last; w0 += MB) {
+      float2 ml[MB][IPT], o[MB][IPT];
+#pragma unroll
+      for (int i = 0; i < MB; ++i) {
+#pragma unroll
+        for (int k = 0; k < IPT; ++k) {
+          ml[i][k] = make_float2(-INFINITY, 0.f);
+          o[i][k] = make_float2(0.f, 0.f);
+        }
+        if (w0 + i <= w_last) {               // uniform: the batch's pieces only
+          const int w = w0 + i;
+          const int64_t base = ((int64_t)w * 2 + (w == w_first ? first_slot : 0)) * p.H;
+#pragma unroll
+          for (int k = 0; k < IPT; ++k) {
+            ml[i][k] = load_pair_agent(p.part_ml + (base + hh[k]) * 2);
+            o[i][k] = load_pair_agent(p.part_o + (base + hh[k]) * D + dd[k]);
+          }
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < IPT; ++k) {
+        float Mn = M[k];
+#pragma unroll
+        for (int i = 0; i < MB; ++i) Mn = fmaxf(Mn, ml[i][k].x);
+        const float a = __builtin_amdgcn_exp2f(M[k] - Mn);   // 0 for the first batch (M = -inf)
+        Lsum[k] *= a;
+        O[k].x *= a;
+        O[k].y *= a;
+#pragma unroll
+        for (int i = 0; i < MB; ++i) {
+          const float sc = __builtin_amdgcn_exp2f(ml[i][k].x - Mn);   // 0 past the last piece
+          Lsum[k] += sc * ml[i][k].y;
+          O[k].x += sc * o[i][k].x;
+          O[k].y += sc * o[i][k].y;
+        }
+        M[k] = Mn;
       }
     }
-    const int64_t off = (int64_t)b * p.out_seq_stride + (int64_t)h * p.out_head_stride + d;
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      if (p.out_f16) reinterpret_cast<uint16_t*>(p.out)[off + k] = f2h(r[k]);
-      else reinterpret_cast<float*>(p.out)[off + k] = r[k];
+    for (int k = 0; k < IPT; ++k) {
+      if (e0 + k * NT >= total) continue;
+      const int h = hh[k], d = dd[k];
+      const float rL = __builtin_amdgcn_rcpf(Lsum[k]);
+      float r[2] = {O[k].x * rL, O[k].y * rL};
+      if constexpr (MODE == SRC_CHANNEL) {
+        if (p.use_quant) {
+          const int64_t kvg = h / G;
+#pragma unroll
+          for (int j = 0; j < 2; ++j) r[j] = h2f(p.vr0[kvg * D + d + j]) * (r[j] - h2f(p.vr1[kvg * D + d + j]));
+        }
+      }
+      const int64_t off = (int64_t)b * p.out_seq_stride + (int64_t)h * p.out_head_stride + d;
+      if (p.out_f16) {
+        reinterpret_cast<uint16_t*>(p.out)[off] = f2h(r[0]);
+        reinterpret_cast<uint16_t*>(p.out)[off + 1] = f2h(r[1]);
+      } else {
+        reinterpret_cast<float*>(p.out)[off] = r[0];
+        reinterpret_cast<float*>(p.out)[off + 1] = r[1];
+      }
     }
   }
   if (tid == 0)

@@ -37,6 +37,12 @@
 // as sum(p * min).  The 4 groups' partial sums are added at the end of a
 // segment.  PV of a tile runs one iteration after its QK, from V words read
 // into registers with the tile's keys.
+//
+// Weights never go through LDS: the 16 QK lanes of a row hold the weights of
+// exactly the tokens that the PV lanes of the same row need.  A DPP move packs
+// the fp16 weights of tokens p and p+1 into one dword (lane of token p), and
+// every PV product reads its weight pair from the source lane of its row with
+// a row_newbcast DPP operand.
 #include "attention_kernel.h"
 
 #include <algorithm>
@@ -70,16 +76,40 @@ struct Shape {
   static constexpr int ROUNDS = TT / 16;                  // QK rounds of 16 tokens
   static constexpr int NP = TT / 8;                       // PV token pairs per lane
   static constexpr int STAGE = TT * RSTRIDE;
-  static constexpr int WSLOT = TT * 8;                    // weight bytes per tile: [pair][head] fp16 x 2
-  static_assert(NS * WSLOT <= 1024, "weight slots must fit the 1 KB scratch");
   static constexpr int QOFF = NS * STAGE;                 // one 1 KB query slot per wave
-  static constexpr int WOFF = QOFF + WAVES * 1024;        // per-wave limb / weight scratch
+  static constexpr int WOFF = QOFF + WAVES * 1024;        // per-wave query-limb scratch
   static constexpr int MOFF = WOFF + WAVES * 1024;        // misc ints
   static constexpr int LDS = MOFF + 32 * 4;
   static_assert(LDS <= 160 * 1024, "LDS ring too large");
 };
 
 constexpr float kC = 1.4426950408889634f / 11.313708498984761f;   // log2(e) / sqrt(128)
+
+// acc[h] += dot(w of lane 8*I + h of this row, v) for the 4 heads h, for
+// both accumulator sets (a: low nibbles, b: whole bytes).  DPP reads of a
+// register written by the previous VALU instruction need two wait states,
+// which the compiler does not insert for inline asm: hence the s_nop.
+template <int I>
+__device__ __forceinline__ void dot2c_bcast4(float& a0, float& a1, float& a2, float& a3, float& b0, float& b1,
+                                             float& b2, float& b3, uint32_t w, uint32_t vlo, uint32_t vfull) {
+  asm("s_nop 1\n\t"
+      "v_dot2c_f32_f16_dpp %0, %8, %9 row_newbcast:%11 row_mask:0xf bank_mask:0xf\n\t"
+      "v_dot2c_f32_f16_dpp %4, %8, %10 row_newbcast:%11 row_mask:0xf bank_mask:0xf\n\t"
+      "v_dot2c_f32_f16_dpp %1, %8, %9 row_newbcast:%12 row_mask:0xf bank_mask:0xf\n\t"
+      "v_dot2c_f32_f16_dpp %5, %8, %10 row_newbcast:%12 row_mask:0xf bank_mask:0xf\n\t"
+      "v_dot2c_f32_f16_dpp %2, %8, %9 row_newbcast:%13 row_mask:0xf bank_mask:0xf\n\t"
+      "v_dot2c_f32_f16_dpp %6, %8, %10 row_newbcast:%13 row_mask:0xf bank_mask:0xf\n\t"
+      "v_dot2c_f32_f16_dpp %3, %8, %9 row_newbcast:%14 row_mask:0xf bank_mask:0xf\n\t"
+      "v_dot2c_f32_f16_dpp %7, %8, %10 row_newbcast:%14 row_mask:0xf bank_mask:0xf"
+      : "+v"(a0), "+v"(a1), "+v"(a2), "+v"(a3), "+v"(b0), "+v"(b1), "+v"(b2), "+v"(b3)
+      : "v"(w), "v"(vlo), "v"(vfull), "n"(8 * I), "n"(8 * I + 1), "n"(8 * I + 2), "n"(8 * I + 3));
+}
+
+// x *= s in x's own register: a conditionally rescaled accumulator then stays
+// in one register on both paths of the branch (no copies on the common path).
+__device__ __forceinline__ void scale_in_place(float& x, float s) {
+  asm volatile("v_mul_f32 %0, %1, %0" : "+v"(x) : "s"(s));
+}
 
 template <int NKV, int WPK, int TT>
 __global__ void __launch_bounds__(NKV * WPK * 64) rows_kernel(const AttnParams p) {
@@ -99,7 +129,7 @@ __global__ void __launch_bounds__(NKV * WPK * 64) rows_kernel(const AttnParams p
   uint8_t* const wscr = smem + S::WOFF + wave * 1024;
 
   TileRange rng;
-  if (!schedule_range<TT, D>(p, misc, h0, h1, rng)) return;
+  if (!schedule_range<TT, D, false>(p, misc, h0, h1, rng)) return;
   const int T = rng.T, Weff = rng.Weff, lo = rng.lo, hi = rng.hi;
 
   // ---------------------------------------------------------------- loads
@@ -136,30 +166,40 @@ __global__ void __launch_bounds__(NKV * WPK * 64) rows_kernel(const AttnParams p
   int dinfo = 0, dchunk = lo;
   int cb = rng.b, cP = rng.Pb;                  // a sequence at or before the next chunk's first tile
   auto build = [&](int first) {
-    int b = cb, P = cP;
-    int L = seq_len_of(p, b), Tb = tiles_of<TT>(L);
-    while (first >= P + Tb && b + 1 < p.B) {
-      P += Tb;
-      ++b;
-      L = seq_len_of(p, b);
-      Tb = tiles_of<TT>(L);
-    }
-    cb = b;
-    cP = P;
+    // Lane j takes sequence b0 + j: its length (one vector load for the 64
+    // sequences) and, by a wave scan, its first tile; then every sequence
+    // that overlaps tiles [first, first + 64) hands its tiles to their lanes.
     const int t = first + lane;
     int mb = -1, mtb = 0, mL = 0, mTb = 0;
+    int b0 = cb, P0 = cP;
     for (;;) {
-      if (t >= P && t < P + Tb) {
-        mb = b;
-        mtb = t - P;
-        mL = L;
-        mTb = Tb;
+      const int Ll = seq_len_lane(p, b0 + lane);   // 0 past the last sequence
+      const int Tl = tiles_of<TT>(Ll);
+      int incl = Tl;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const int n = __shfl_up(incl, o, 64);
+        if (lane >= o) incl += n;
       }
-      P += Tb;
-      if (!__builtin_amdgcn_ballot_w64(t >= P && t < hi) || b + 1 >= p.B) break;
-      ++b;
-      L = seq_len_of(p, b);
-      Tb = tiles_of<TT>(L);
+      const int sl = P0 + incl - Tl;
+      uint64_t ov = __builtin_amdgcn_ballot_w64(Tl > 0 && sl < first + 64 && sl + Tl > first);
+      while (ov) {
+        const int j = __builtin_ctzll(ov);
+        ov &= ov - 1;
+        const int s0 = __builtin_amdgcn_readlane(sl, j), n = __builtin_amdgcn_readlane(Tl, j);
+        if (t >= s0 && t < s0 + n) {
+          mb = b0 + j;
+          mtb = t - s0;
+          mL = __builtin_amdgcn_readlane(Ll, j);
+          mTb = n;
+        }
+        cb = b0 + j;
+        cP = s0;
+      }
+      const int total = __builtin_amdgcn_readlane(incl, 63);
+      if (P0 + total >= min(first + 64, hi) || b0 + 64 >= p.B) break;
+      b0 += 64;
+      P0 += total;
     }
     uint64_t base = reinterpret_cast<uint64_t>(p.cache);
     dinfo = 0;
@@ -213,7 +253,10 @@ __global__ void __launch_bounds__(NKV * WPK * 64) rows_kernel(const AttnParams p
   // Heads are stored rotated: slot j holds head (qc + j) & 3, so the quad's
   // reduce-scatter needs no per-lane selects.
   uint32_t qlq[4][4][4];              // [head slot][dword][limb]
-  float qa = 0.f, qb = 0.f, m_run = -INFINITY, l_run = 0.f, vmt = 0.f;
+  // Scores are kept in query-integer units, u = step * (qi . n) + min * sum(qi);
+  // qa converts them to base-2 logits (log2(e) / sqrt(D) / query scale), so a
+  // weight is exp2((u - m_run) * qa) and m_run is the running max of u.
+  float qa = 0.f, qb = 0.f, mq = 0.f, m_run = -INFINITY, l_run = 0.f, vmt = 0.f;
   float accl[4][4], accf[4][4];       // [byte k][head]: sum w * lo, sum w * (lo + 16 hi), units of 2^-24
   const int pc = lane & 15, pq = lane >> 4;   // PV: dword column, token group
 
@@ -252,9 +295,9 @@ __global__ void __launch_bounds__(NKV * WPK * 64) rows_kernel(const AttnParams p
 #pragma unroll
       for (int k = 0; k < 4; ++k) limb[k] |= ((qu >> (4 * k)) & 15u) << (4 * i);
     }
-    const float qsum = red16_sum((float)isum) * rsq;    // |sum qi| < 2^24: exact before the scaling
+    const float qsum = red16_sum((float)isum);    // |sum qi| < 2^24: exact
     uint32_t* wl = reinterpret_cast<uint32_t*>(wscr);
-    wave_lds_sync();                     // earlier weight reads of this wave are done
+    wave_lds_sync();                     // earlier limb reads of this wave are done
 #pragma unroll
     for (int k = 0; k < 4; ++k) wl[(qg * 4 + k) * 16 + qp] = limb[k];
     wave_lds_sync();
@@ -272,7 +315,7 @@ __global__ void __launch_bounds__(NKV * WPK * 64) rows_kernel(const AttnParams p
         qlq[j][3][k] = swp ? v.y : v.w;
       }
     qa = kC * rsq;
-    qb = kC * qsum;
+    qb = qsum;
   };
 
   // Score of this lane's token for head qg (base-2 units): the lane's key
@@ -311,7 +354,7 @@ __global__ void __launch_bounds__(NKV * WPK * 64) rows_kernel(const AttnParams p
     const int iacc = (int)z - (int)(sn << 15);
     const float kmin = h2f((uint16_t)(kr.x & 0xffffu));
     const float kstep = h2f((uint16_t)(kr.x >> 16));
-    return ((float)iacc * qa) * kstep + kmin * qb;
+    return (float)iacc * kstep + kmin * qb;
   };
 
   // PV token pairs of this lane's group: pairs P = 8m + 2pq and 8m + 2pq + 1,
@@ -343,28 +386,28 @@ __global__ void __launch_bounds__(NKV * WPK * 64) rows_kernel(const AttnParams p
     }
   };
 
-  // QK and softmax of one tile; its fp16 weights go to the scratch slot `wh`
-  // (dword [pair][head] = (w(2i), w(2i+1))).
-  auto qk_softmax = [&](const uint32_t (&kq)[S::ROUNDS][4], const uint2 (&kr)[S::ROUNDS], int nvalid, uint8_t* wh) {
+  // QK and softmax of one tile.  Its weights w = p * step come back in W:
+  // W[r] of the lane of (token 16r + qp, head qg) with qp even holds the fp16
+  // pair (w(token), w(token + 1)) of head qg.  Tokens past the sequence end
+  // get u = -inf, hence weight exp2(-inf) = 0.
+  auto qk_softmax = [&](const uint32_t (&kq)[S::ROUNDS][4], const uint2 (&kr)[S::ROUNDS], int nvalid,
+                        uint32_t (&W)[S::ROUNDS]) {
     float s2[S::ROUNDS];
-    bool tv[S::ROUNDS];
-    bool any_grow = false;
 #pragma unroll
     for (int r = 0; r < S::ROUNDS; ++r) {
-      tv[r] = 16 * r + qp < nvalid;
       const float sc = score(kq[r], kr[r]);
-      s2[r] = tv[r] ? sc : -INFINITY;
-      any_grow = any_grow || s2[r] > m_run;
+      s2[r] = 16 * r + qp < nvalid ? sc : -INFINITY;
     }
+    float tl = s2[0];
+#pragma unroll
+    for (int r = 1; r < S::ROUNDS; ++r) tl = fmaxf(tl, s2[r]);
     // online softmax: the running max per head is only recomputed (and the
     // sums rescaled) when some score of the tile exceeds it
-    if (__builtin_amdgcn_ballot_w64(any_grow)) {
-      float tl = s2[0];
-#pragma unroll
-      for (int r = 1; r < S::ROUNDS; ++r) tl = fmaxf(tl, s2[r]);
+    if (__builtin_amdgcn_ballot_w64(tl > m_run)) {
       const float tmax = red16_max(tl);
       const bool grow = tmax > m_run;
-      const float alpha = grow ? __builtin_amdgcn_exp2f(m_run - tmax) : 1.f;   // 0 when growing from -inf
+      // 0 when growing from -inf
+      const float alpha = grow ? __builtin_amdgcn_exp2f((m_run - tmax) * qa) : 1.f;
       l_run *= alpha;
       vmt *= alpha;
 #pragma unroll
@@ -372,43 +415,44 @@ __global__ void __launch_bounds__(NKV * WPK * 64) rows_kernel(const AttnParams p
         const float ah = readlane_f(alpha, h);
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-          accl[k][h] *= ah;
-          accf[k][h] *= ah;
+          scale_in_place(accl[k][h], ah);
+          scale_in_place(accf[k][h], ah);
         }
       }
       m_run = grow ? tmax : m_run;
+      mq = m_run * qa;
     }
-    uint16_t* w16 = reinterpret_cast<uint16_t*>(wh);
 #pragma unroll
     for (int r = 0; r < S::ROUNDS; ++r) {
       // m_run > -inf here: token 0 of every tile is valid
-      const float pr = __builtin_amdgcn_exp2f(s2[r] - m_run);
+      const float pr = __builtin_amdgcn_exp2f(__builtin_fmaf(s2[r], qa, -mq));
       const float vmin = h2f((uint16_t)(kr[r].y & 0xffffu));
       const float vstep = h2f((uint16_t)(kr[r].y >> 16));
-      l_run += tv[r] ? pr : 0.f;
-      vmt += tv[r] ? pr * vmin : 0.f;
-      const int tok = 16 * r + qp;
-      w16[((tok >> 1) * 4 + qg) * 2 + (tok & 1)] = f2h(tv[r] ? pr * vstep : 0.f);
+      l_run += pr;
+      vmt = __builtin_fmaf(pr, vmin, vmt);
+      const uint32_t wl = f2h(pr * vstep);
+      W[r] = wl | (dpp_u<DPP_ROW_SHL4>(wl) << 16);   // token qp + 1 is 4 lanes up
     }
   };
 
-  // PV of one tile from its V words and the weights in scratch slot `wh`.
-  auto pv = [&](const uint32_t (&xv)[2 * S::NP], const uint8_t* wh) {
+  // PV of one tile from its V words and its weights W.  Pair j (tokens
+  // 16m + 4pq + 2i and the next, m = j / 2, i = j % 2) has its weights for
+  // head h in W[m] of lane 8i + h of this lane's row.
+  auto pv = [&](const uint32_t (&xv)[2 * S::NP], const uint32_t (&W)[S::ROUNDS]) __attribute__((always_inline)) {
 #pragma unroll
     for (int j = 0; j < S::NP; ++j) {
-      const uint4 wq = *reinterpret_cast<const uint4*>(wh + pair_of(j) * 16);
-      const uint32_t whd[4] = {wq.x, wq.y, wq.z, wq.w};
-      const uint32_t x0 = xv[2 * j], x1 = xv[2 * j + 1];
+      const uint32_t x0 = xv[2 * j], x1 = xv[2 * j + 1], w = W[j >> 1];
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
         // byte k of both tokens at bits 0-7 and 16-23
         const uint32_t tw = __builtin_amdgcn_perm(x1, x0, 0x0C000C00u | ((4u + k) << 16) | (uint32_t)k);
         const uint32_t vlo = tw & 0x000F000Fu;
-#pragma unroll
-        for (int h = 0; h < 4; ++h) {
-          accl[k][h] = fdot2(whd[h], vlo, accl[k][h]);
-          accf[k][h] = fdot2(whd[h], tw, accf[k][h]);
-        }
+        if (j & 1)
+          dot2c_bcast4<1>(accl[k][0], accl[k][1], accl[k][2], accl[k][3], accf[k][0], accf[k][1], accf[k][2],
+                          accf[k][3], w, vlo, tw);
+        else
+          dot2c_bcast4<0>(accl[k][0], accl[k][1], accl[k][2], accl[k][3], accf[k][0], accf[k][1], accf[k][2],
+                          accf[k][3], w, vlo, tw);
       }
     }
   };
@@ -465,7 +509,8 @@ __global__ void __launch_bounds__(NKV * WPK * 64) rows_kernel(const AttnParams p
       const int64_t pbase = ((int64_t)wg * 2 + slot) * p.H;
 #pragma unroll
       for (int h = 0; h < 4; ++h) store_pair_agent(p.part_o + (pbase + hw + h) * D + dcol, o[h][0], o[h][1]);
-      if (lane < 4) store_pair_agent(p.part_ml + (pbase + hw + lane) * 2, m_run, lt);   // lane g: head g
+      // lane g: head g; the running max in base-2 logits
+      if (lane < 4) store_pair_agent(p.part_ml + (pbase + hw + lane) * 2, m_run * qa, lt);
       const int L = seq_len_of(p, b);
       const int Pb = whole ? seg_first : rng.Pb;
       if (npend == 0) {
@@ -502,10 +547,13 @@ __global__ void __launch_bounds__(NKV * WPK * 64) rows_kernel(const AttnParams p
   sinfo[1] = lo + 1 < hi ? issue(lo + 1, 1) : 0;
   int seg_first = lo;
   bool seg_whole = false;
-  uint32_t xvp[2 * S::NP];      // V words of the previous tile
+  uint32_t xvs[2][2 * S::NP];   // V words of the tiles in the two stages
+  uint32_t Ws[2][S::ROUNDS];    // their weights
   int pinfo = 0;                // info of the previous tile
 #pragma unroll
-  for (int i = 0; i < 2 * S::NP; ++i) xvp[i] = 0;
+  for (int i = 0; i < 2 * S::NP; ++i) xvs[0][i] = xvs[1][i] = 0;
+#pragma unroll
+  for (int i = 0; i < S::ROUNDS; ++i) Ws[0][i] = Ws[1][i] = 0;
 
   auto iteration = [&](int t, auto stage) {
     constexpr int st = decltype(stage)::value;
@@ -516,13 +564,13 @@ __global__ void __launch_bounds__(NKV * WPK * 64) rows_kernel(const AttnParams p
     const int info = sinfo[st];
     const bool first_of_seq = (info >> 7) & 1;
     const bool seg_start = t == lo || first_of_seq;
-    uint32_t kq[S::ROUNDS][4], xv[2 * S::NP];
+    uint32_t kq[S::ROUNDS][4];
     uint2 kr[S::ROUNDS];
-    read_tile(smem + st * S::STAGE + kvw * SLOT, kq, kr, xv);
+    read_tile(smem + st * S::STAGE + kvw * SLOT, kq, kr, xvs[st]);
     uint4 qw = make_uint4(0u, 0u, 0u, 0u);
     if (seg_start) qw = *reinterpret_cast<const uint4*>(smem + S::QOFF + wave * 1024 + lane * 16);
     if (t > lo) {
-      pv(xvp, wscr + so * S::WSLOT);
+      pv(xvs[so], Ws[so]);
       if ((pinfo >> 6) & 1) finish(pinfo >> 8, seg_first, seg_whole, true);
     }
     lds_barrier();
@@ -548,21 +596,21 @@ __global__ void __launch_bounds__(NKV * WPK * 64) rows_kernel(const AttnParams p
       begin(qw);
     }
     if (more) loads(nx, IC1{}, IC2{});
-    qk_softmax(kq, kr, (info & 63) + 1, wscr + st * S::WSLOT);
+    qk_softmax(kq, kr, (info & 63) + 1, Ws[st]);
     if (more) loads(nx, IC2{}, IC3{});
-#pragma unroll
-    for (int i = 0; i < 2 * S::NP; ++i) xvp[i] = xv[i];
     pinfo = info;
   };
   for (int t = lo; t < hi; t += 2) {
     iteration(t, std::integral_constant<int, 0>{});
     if (t + 1 < hi) iteration(t + 1, std::integral_constant<int, 1>{});
   }
-  // the range's last tile: its weights are in this wave's scratch (the wave's
-  // own LDS writes are ordered before its reads)
-  wave_lds_sync();
-  pv(xvp, wscr + ((hi - 1 - lo) & 1) * S::WSLOT);
+  // the range's last tile
+  if ((hi - 1 - lo) & 1) pv(xvs[1], Ws[1]);
+  else pv(xvs[0], Ws[0]);
   finish(pinfo >> 8, seg_first, seg_whole, (pinfo >> 6) & 1);
+
+  // outputs of empty sequences (off the prologue's critical path)
+  zero_empty<D>(p, h0, h1, Weff);
 
   // ---------------------------------------------------------------- arrivals and merges
   if (npend == 0) return;

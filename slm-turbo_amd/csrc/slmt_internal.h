@@ -41,6 +41,7 @@ enum : int {
   DPP_QUAD_ROT3 = 0x93,   // quad_perm [3,0,1,2]: lane i reads lane (i+3) & 3
   DPP_ROW_ROR4 = 0x124,
   DPP_ROW_ROR8 = 0x128,
+  DPP_ROW_SHL4 = 0x104,   // lane i reads lane i+4 of its row (0 past the row's end)
 };
 
 // Every control used here (quad permutations, rotations within a row) reads
