@@ -325,7 +325,7 @@ __device__ bool schedule_range(const AttnParams& p, int* misc, int h0, int h1, T
 // thread merges IPT items at once, MB pieces per batch, with all of a batch's
 // loads issued together, and updates the running maximum once per batch.  For
 // the per-channel layout the V scale/zero are applied to the merged average.
-template <int D, int MODE>
+template <int D, int MODE, bool RESET = true>
 __device__ void merge_sequence(const AttnParams& p, int b, int Pb, int Tb, int T, int Weff, int h0, int h1,
                                int group) {
   static_assert(D % 2 == 0, "work items of 2 dims");
@@ -409,7 +409,8 @@ __device__ void merge_sequence(const AttnParams& p, int b, int Pb, int Tb, int T
       }
     }
   }
-  if (tid == 0)
+  // RESET: re-arm the arrival counter of (group, b) for the next call
+  if (RESET && tid == 0)
     __hip_atomic_store(p.counters + (int64_t)group * p.B + b, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
@@ -825,11 +826,10 @@ __global__ void __launch_bounds__(MAX_THREADS) attention_kernel(const AttnParams
   const int h1 = min(p.H, h0 + p.heads_per_group);
   const int kv_lo = h0 / G;
   const int nkv = (h1 - 1) / G - kv_lo + 1;
-  // this wave's heads [hw0, hw1) (none for trailing waves of a short last group)
+  // this wave's heads [hw0, min(h1, hwa + 4)) (none for trailing waves of a short last group)
   const int hw0 = h0 + 4 * wave;
   const bool active = hw0 < h1;
   const int hwa = active ? hw0 : h1 - 1;
-  const int hw1 = min(h1, hwa + 4);
   const LdsGeom geo = lds_geom(nkv, D, nwaves);
   const DmaGeom dgeo = dma_geom(D, nwaves);
   constexpr int UNITS = dma_units(D), OPS = dma_ops(D), SPLIT = dma_split(D), ISSUES = dma_issues(D);

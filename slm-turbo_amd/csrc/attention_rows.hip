@@ -56,7 +56,7 @@ namespace rows {
 
 using namespace attn;
 
-constexpr int D = 128, SLOT = D + 8, KD = D / 8;
+constexpr int D = 128, SLOT = D + 8;
 
 template <int NKV, int WPK, int TT>
 struct Shape {
@@ -85,24 +85,50 @@ struct Shape {
 
 constexpr float kC = 1.4426950408889634f / 11.313708498984761f;   // log2(e) / sqrt(128)
 
-// acc[h] += dot(w of lane 8*I + h of this row, v) for the 4 heads h, for
-// both accumulator sets (a: low nibbles, b: whole bytes).  DPP reads of a
+// One token pair's PV products: al[k][h] += dot(w of lane 8*I + h of this
+// row, lo[k]) and af[k][h] += dot(that w, fu[k]) for bytes k and heads h, 32
+// independent products behind one wait for the DPP read of w (DPP reads of a
 // register written by the previous VALU instruction need two wait states,
-// which the compiler does not insert for inline asm: hence the s_nop.
+// which the compiler does not insert for inline asm).
 template <int I>
-__device__ __forceinline__ void dot2c_bcast4(float& a0, float& a1, float& a2, float& a3, float& b0, float& b1,
-                                             float& b2, float& b3, uint32_t w, uint32_t vlo, uint32_t vfull) {
+__device__ __forceinline__ void pv_pair_bcast(float (&al)[4][4], float (&af)[4][4], uint32_t w, const uint32_t (&lo)[4],
+                                              const uint32_t (&fu)[4]) {
   asm("s_nop 1\n\t"
-      "v_dot2c_f32_f16_dpp %0, %8, %9 row_newbcast:%11 row_mask:0xf bank_mask:0xf\n\t"
-      "v_dot2c_f32_f16_dpp %4, %8, %10 row_newbcast:%11 row_mask:0xf bank_mask:0xf\n\t"
-      "v_dot2c_f32_f16_dpp %1, %8, %9 row_newbcast:%12 row_mask:0xf bank_mask:0xf\n\t"
-      "v_dot2c_f32_f16_dpp %5, %8, %10 row_newbcast:%12 row_mask:0xf bank_mask:0xf\n\t"
-      "v_dot2c_f32_f16_dpp %2, %8, %9 row_newbcast:%13 row_mask:0xf bank_mask:0xf\n\t"
-      "v_dot2c_f32_f16_dpp %6, %8, %10 row_newbcast:%13 row_mask:0xf bank_mask:0xf\n\t"
-      "v_dot2c_f32_f16_dpp %3, %8, %9 row_newbcast:%14 row_mask:0xf bank_mask:0xf\n\t"
-      "v_dot2c_f32_f16_dpp %7, %8, %10 row_newbcast:%14 row_mask:0xf bank_mask:0xf"
-      : "+v"(a0), "+v"(a1), "+v"(a2), "+v"(a3), "+v"(b0), "+v"(b1), "+v"(b2), "+v"(b3)
-      : "v"(w), "v"(vlo), "v"(vfull), "n"(8 * I), "n"(8 * I + 1), "n"(8 * I + 2), "n"(8 * I + 3));
+      "v_dot2c_f32_f16_dpp %0, %32, %33 row_newbcast:%41 row_mask:0xf bank_mask:0xf\n\t"
+      "v_dot2c_f32_f16_dpp %16, %32, %37 row_newbcast:%41 row_mask:0xf bank_mask:0xf\n\t"
+      "v_dot2c_f32_f16_dpp %4, %32, %34 row_newbcast:%41 row_mask:0xf bank_mask:0xf\n\t"
+      "v_dot2c_f32_f16_dpp %20, %32, %38 row_newbcast:%41 row_mask:0xf bank_mask:0xf\n\t"
+      "v_dot2c_f32_f16_dpp %8, %32, %35 row_newbcast:%41 row_mask:0xf bank_mask:0xf\n\t"
+      "v_dot2c_f32_f16_dpp %24, %32, %39 row_newbcast:%41 row_mask:0xf bank_mask:0xf\n\t"
+      "v_dot2c_f32_f16_dpp %12, %32, %36 row_newbcast:%41 row_mask:0xf bank_mask:0xf\n\t"
+      "v_dot2c_f32_f16_dpp %28, %32, %40 row_newbcast:%41 row_mask:0xf bank_mask:0xf\n\t"
+      "v_dot2c_f32_f16_dpp %1, %32, %33 row_newbcast:%42 row_mask:0xf bank_mask:0xf\n\t"
+      "v_dot2c_f32_f16_dpp %17, %32, %37 row_newbcast:%42 row_mask:0xf bank_mask:0xf\n\t"
+      "v_dot2c_f32_f16_dpp %5, %32, %34 row_newbcast:%42 row_mask:0xf bank_mask:0xf\n\t"
+      "v_dot2c_f32_f16_dpp %21, %32, %38 row_newbcast:%42 row_mask:0xf bank_mask:0xf\n\t"
+      "v_dot2c_f32_f16_dpp %9, %32, %35 row_newbcast:%42 row_mask:0xf bank_mask:0xf\n\t"
+      "v_dot2c_f32_f16_dpp %25, %32, %39 row_newbcast:%42 row_mask:0xf bank_mask:0xf\n\t"
+      "v_dot2c_f32_f16_dpp %13, %32, %36 row_newbcast:%42 row_mask:0xf bank_mask:0xf\n\t"
+      "v_dot2c_f32_f16_dpp %29, %32, %40 row_newbcast:%42 row_mask:0xf bank_mask:0xf\n\t"
+      "v_dot2c_f32_f16_dpp %2, %32, %33 row_newbcast:%43 row_mask:0xf bank_mask:0xf\n\t"
+      "v_dot2c_f32_f16_dpp %18, %32, %37 row_newbcast:%43 row_mask:0xf bank_mask:0xf\n\t"
+      "v_dot2c_f32_f16_dpp %6, %32, %34 row_newbcast:%43 row_mask:0xf bank_mask:0xf\n\t"
+      "v_dot2c_f32_f16_dpp %22, %32, %38 row_newbcast:%43 row_mask:0xf bank_mask:0xf\n\t"
+      "v_dot2c_f32_f16_dpp %10, %32, %35 row_newbcast:%43 row_mask:0xf bank_mask:0xf\n\t"
+      "v_dot2c_f32_f16_dpp %26, %32, %39 row_newbcast:%43 row_mask:0xf bank_mask:0xf\n\t"
+      "v_dot2c_f32_f16_dpp %14, %32, %36 row_newbcast:%43 row_mask:0xf bank_mask:0xf\n\t"
+      "v_dot2c_f32_f16_dpp %30, %32, %40 row_newbcast:%43 row_mask:0xf bank_mask:0xf\n\t"
+      "v_dot2c_f32_f16_dpp %3, %32, %33 row_newbcast:%44 row_mask:0xf bank_mask:0xf\n\t"
+      "v_dot2c_f32_f16_dpp %19, %32, %37 row_newbcast:%44 row_mask:0xf bank_mask:0xf\n\t"
+      "v_dot2c_f32_f16_dpp %7, %32, %34 row_newbcast:%44 row_mask:0xf bank_mask:0xf\n\t"
+      "v_dot2c_f32_f16_dpp %23, %32, %38 row_newbcast:%44 row_mask:0xf bank_mask:0xf\n\t"
+      "v_dot2c_f32_f16_dpp %11, %32, %35 row_newbcast:%44 row_mask:0xf bank_mask:0xf\n\t"
+      "v_dot2c_f32_f16_dpp %27, %32, %39 row_newbcast:%44 row_mask:0xf bank_mask:0xf\n\t"
+      "v_dot2c_f32_f16_dpp %15, %32, %36 row_newbcast:%44 row_mask:0xf bank_mask:0xf\n\t"
+      "v_dot2c_f32_f16_dpp %31, %32, %40 row_newbcast:%44 row_mask:0xf bank_mask:0xf"
+      : "+v"(al[0][0]), "+v"(al[0][1]), "+v"(al[0][2]), "+v"(al[0][3]), "+v"(al[1][0]), "+v"(al[1][1]), "+v"(al[1][2]), "+v"(al[1][3]), "+v"(al[2][0]), "+v"(al[2][1]), "+v"(al[2][2]), "+v"(al[2][3]), "+v"(al[3][0]), "+v"(al[3][1]), "+v"(al[3][2]), "+v"(al[3][3]), "+v"(af[0][0]), "+v"(af[0][1]), "+v"(af[0][2]), "+v"(af[0][3]), "+v"(af[1][0]), "+v"(af[1][1]), "+v"(af[1][2]), "+v"(af[1][3]), "+v"(af[2][0]), "+v"(af[2][1]), "+v"(af[2][2]), "+v"(af[2][3]), "+v"(af[3][0]), "+v"(af[3][1]), "+v"(af[3][2]), "+v"(af[3][3])
+      : "v"(w), "v"(lo[0]), "v"(lo[1]), "v"(lo[2]), "v"(lo[3]), "v"(fu[0]), "v"(fu[1]), "v"(fu[2]), "v"(fu[3]),
+        "n"(8 * I), "n"(8 * I + 1), "n"(8 * I + 2), "n"(8 * I + 3));
 }
 
 // x *= s in x's own register: a conditionally rescaled accumulator then stays
@@ -130,7 +156,7 @@ __global__ void __launch_bounds__(NKV * WPK * 64) rows_kernel(const AttnParams p
 
   TileRange rng;
   if (!schedule_range<TT, D, false>(p, misc, h0, h1, rng)) return;
-  const int T = rng.T, Weff = rng.Weff, lo = rng.lo, hi = rng.hi;
+  const int lo = rng.lo, hi = rng.hi;
 
   // ---------------------------------------------------------------- loads
   // The wave copies rows rw0 .. rw0+RW-1 of each tile, consecutive rows of one
@@ -441,26 +467,18 @@ __global__ void __launch_bounds__(NKV * WPK * 64) rows_kernel(const AttnParams p
   auto pv = [&](const uint32_t (&xv)[2 * S::NP], const uint32_t (&W)[S::ROUNDS]) __attribute__((always_inline)) {
 #pragma unroll
     for (int j = 0; j < S::NP; ++j) {
-      const uint32_t x0 = xv[2 * j], x1 = xv[2 * j + 1], w = W[j >> 1];
+      const uint32_t x0 = xv[2 * j], x1 = xv[2 * j + 1];
+      uint32_t lo[4], fu[4];
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
         // byte k of both tokens at bits 0-7 and 16-23
-        const uint32_t tw = __builtin_amdgcn_perm(x1, x0, 0x0C000C00u | ((4u + k) << 16) | (uint32_t)k);
-        const uint32_t vlo = tw & 0x000F000Fu;
-        if (j & 1)
-          dot2c_bcast4<1>(accl[k][0], accl[k][1], accl[k][2], accl[k][3], accf[k][0], accf[k][1], accf[k][2],
-                          accf[k][3], w, vlo, tw);
-        else
-          dot2c_bcast4<0>(accl[k][0], accl[k][1], accl[k][2], accl[k][3], accf[k][0], accf[k][1], accf[k][2],
-                          accf[k][3], w, vlo, tw);
+        fu[k] = __builtin_amdgcn_perm(x1, x0, 0x0C000C00u | ((4u + k) << 16) | (uint32_t)k);
+        lo[k] = fu[k] & 0x000F000Fu;
       }
+      if (j & 1) pv_pair_bcast<1>(accl, accf, W[j >> 1], lo, fu);
+      else pv_pair_bcast<0>(accl, accf, W[j >> 1], lo, fu);
     }
   };
-
-  // Pending partial pieces, counted after the range (at most two: the range's
-  // first and last segments): sequence, first tile, tiles.
-  int npend = 0;
-  int pb0 = 0, pP0 = 0, pT0 = 0, pb1 = 0, pP1 = 0, pT1 = 0;
 
   // End of a segment of sequence b whose first tile is seg_first (a whole
   // sequence when `whole`): add the token groups' sums and write the output
@@ -511,18 +529,6 @@ __global__ void __launch_bounds__(NKV * WPK * 64) rows_kernel(const AttnParams p
       for (int h = 0; h < 4; ++h) store_pair_agent(p.part_o + (pbase + hw + h) * D + dcol, o[h][0], o[h][1]);
       // lane g: head g; the running max in base-2 logits
       if (lane < 4) store_pair_agent(p.part_ml + (pbase + hw + lane) * 2, m_run * qa, lt);
-      const int L = seq_len_of(p, b);
-      const int Pb = whole ? seg_first : rng.Pb;
-      if (npend == 0) {
-        pb0 = b;
-        pP0 = Pb;
-        pT0 = tiles_of<TT>(L);
-      } else {
-        pb1 = b;
-        pP1 = Pb;
-        pT1 = tiles_of<TT>(L);
-      }
-      ++npend;
     }
   };
 
@@ -609,26 +615,53 @@ __global__ void __launch_bounds__(NKV * WPK * 64) rows_kernel(const AttnParams p
   else pv(xvs[0], Ws[0]);
   finish(pinfo >> 8, seg_first, seg_whole, (pinfo >> 6) & 1);
 
-  // outputs of empty sequences (off the prologue's critical path)
-  zero_empty<D>(p, h0, h1, Weff);
+  // Split sequences are merged, and empty sequences zeroed, by merge_kernel,
+  // launched after this kernel on the same stream.
+}
 
-  // ---------------------------------------------------------------- arrivals and merges
-  if (npend == 0) return;
-  vm_drain();       // this wave's partial stores are complete (agent-coherent)
-  __syncthreads();
-  auto arrive = [&](int b, int Pb, int Tb) -> int {
-    const int pieces = range_owner(Pb + Tb - 1, T, Weff) - range_owner(Pb, T, Weff) + 1;
-    const int prev = __hip_atomic_fetch_add(p.counters + (int64_t)group * p.B + b, 1, __ATOMIC_RELAXED,
-                                            __HIP_MEMORY_SCOPE_AGENT);
-    return (prev == pieces - 1) ? 1 : 0;
-  };
-  if (tid == 0) {
-    misc[24] = arrive(pb0, pP0, pT0);
-    misc[25] = npend > 1 ? arrive(pb1, pP1, pT1) : 0;
+// Merge of the split sequences, one workgroup per (sequence, MH heads):
+// recomputes the stream-K split of the decode launch (the same tile counts,
+// total T and workgroup count Weff from the same parameters) and, when the
+// sequence spans several workgroups, combines their (m, l, o) partials.
+// Empty sequences get zeros here.  The decode kernel's partial stores are
+// visible because this kernel runs after it on the same stream.
+constexpr int MH = 8;   // heads per merge workgroup
+template <int TT>
+__global__ void __launch_bounds__(128) merge_kernel(const AttnParams p) {
+  const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int h0 = blockIdx.y * MH, h1 = min(p.H, h0 + MH);
+  __shared__ int red[4];
+  // tiles before sequence b and in total
+  int pre = 0, tot = 0;
+  for (int i = tid; i < p.B; i += blockDim.x) {
+    const int t = tiles_of<TT>(seq_len_lane(p, i));
+    tot += t;
+    pre += i < b ? t : 0;
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    pre += __shfl_xor(pre, o, 64);
+    tot += __shfl_xor(tot, o, 64);
+  }
+  if (lane == 0) {
+    red[wave] = pre;
+    red[2 + wave] = tot;
   }
   __syncthreads();
-  if (misc[24]) merge_sequence<D, SRC_PAGED>(p, pb0, pP0, pT0, T, Weff, h0, h1, group);
-  if (misc[25]) merge_sequence<D, SRC_PAGED>(p, pb1, pP1, pT1, T, Weff, h0, h1, group);
+  const int Pb = red[0] + red[1], T = red[2] + red[3];
+  const int L = seq_len_of(p, b);
+  if (L == 0) {
+    for (int e = tid; e < (h1 - h0) * D; e += blockDim.x) {
+      const int64_t o = (int64_t)b * p.out_seq_stride + (int64_t)(h0 + e / D) * p.out_head_stride + e % D;
+      if (p.out_f16) reinterpret_cast<uint16_t*>(p.out)[o] = 0;
+      else reinterpret_cast<float*>(p.out)[o] = 0.0f;
+    }
+    return;
+  }
+  const int Tb = tiles_of<TT>(L);
+  const int Weff = max(1, min(p.W, (T + p.min_tiles - 1) / p.min_tiles));
+  if (range_owner(Pb, T, Weff) == range_owner(Pb + Tb - 1, T, Weff)) return;   // one workgroup wrote it
+  merge_sequence<D, SRC_PAGED, false>(p, b, Pb, Tb, T, Weff, h0, h1, 0);
 }
 
 // Workgroups one CU holds at once (cached per kernel; 0 if unknown).
@@ -659,7 +692,12 @@ static int launch(AttnParams p, int groups, hipStream_t stream) {
   p.nthreads = S::THREADS;
   p.heads_per_group = 4 * S::WAVES;
   hipLaunchKernelGGL(kern, dim3(W, groups), dim3(S::THREADS), S::LDS, stream, p);
-  return check_launch("paged decode");
+  if (int rc = check_launch("paged decode")) return rc;
+  if (p.B > 0) {
+    hipLaunchKernelGGL(merge_kernel<TT>, dim3(p.B, (p.H + MH - 1) / MH), dim3(128), 0, stream, p);
+    return check_launch("paged decode merge");
+  }
+  return 0;
 }
 
 }  // namespace rows
