@@ -325,11 +325,19 @@ __device__ bool schedule_range(const AttnParams& p, int* misc, int h0, int h1, T
 // thread merges IPT items at once, MB pieces per batch, with all of a batch's
 // loads issued together, and updates the running maximum once per batch.  For
 // the per-channel layout the V scale/zero are applied to the merged average.
-template <int D, int MODE, bool RESET = true>
+// IN_KERNEL: the pieces come from workgroups of the running kernel (read
+// agent-coherently, arrival counter re-armed at the end); otherwise from a
+// kernel that ran before this one on the same stream (plain loads, 8 pieces
+// per batch).
+template <int D, int MODE, bool IN_KERNEL = true>
 __device__ void merge_sequence(const AttnParams& p, int b, int Pb, int Tb, int T, int Weff, int h0, int h1,
                                int group) {
   static_assert(D % 2 == 0, "work items of 2 dims");
-  constexpr int MB = 4, IPT = 4;
+  constexpr int MB = IN_KERNEL ? 4 : 8, IPT = 4;
+  auto load2 = [&](const float* src) -> float2 {
+    if constexpr (IN_KERNEL) return load_pair_agent(src);
+    else return *reinterpret_cast<const float2*>(src);
+  };
   const int tid = threadIdx.x, NT = blockDim.x, G = p.G;
   const int w_first = range_owner(Pb, T, Weff);
   const int w_last = range_owner(Pb + Tb - 1, T, Weff);
@@ -362,8 +370,8 @@ __device__ void merge_sequence(const AttnParams& p, int b, int Pb, int Tb, int T
           const int64_t base = ((int64_t)w * 2 + (w == w_first ? first_slot : 0)) * p.H;
 #pragma unroll
           for (int k = 0; k < IPT; ++k) {
-            ml[i][k] = load_pair_agent(p.part_ml + (base + hh[k]) * 2);
-            o[i][k] = load_pair_agent(p.part_o + (base + hh[k]) * D + dd[k]);
+            ml[i][k] = load2(p.part_ml + (base + hh[k]) * 2);
+            o[i][k] = load2(p.part_o + (base + hh[k]) * D + dd[k]);
           }
         }
       }
@@ -409,8 +417,7 @@ __device__ void merge_sequence(const AttnParams& p, int b, int Pb, int Tb, int T
       }
     }
   }
-  // RESET: re-arm the arrival counter of (group, b) for the next call
-  if (RESET && tid == 0)
+  if (IN_KERNEL && tid == 0)
     __hip_atomic_store(p.counters + (int64_t)group * p.B + b, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
