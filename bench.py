@@ -10,12 +10,17 @@ dequant + attention over the whole batch; inputs are resident in HBM.  Three
 independent caches and queries (~303 MB of KV each, together above the 256 MB
 Infinity Cache) are rotated so no step is served from it.
 
+Steady state: a freshly started process needs about 200 back-to-back decode
+launches (~20 ms) before the GPU settles (the first ~100 launches run ~20 %
+slower).  Before its W warmup steps, the benchmark therefore runs the decode
+untimed for --prewarm-ms (default 100 ms); the JSON line reports it.
+
 Printed: one JSON line with the throughput in algorithmic GB/s (packed KV +
 rulers, q, fp32 out, block-table entries and lengths actually read), the time
 per step, the roofline object for the decode kernel and a CPU baseline (the
 reference's CPU torch path on a bounded sample of the same workload).
 
-    python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--no-cpu]
+    python bench.py [--gpus 1] [--steps 500] [--warmup 400] [--prewarm-ms 100] [--no-cpu]
 """
 from __future__ import annotations
 
@@ -43,8 +48,10 @@ TRAFFIC_FILE = ROOT / "profiles" / "paged_decode_b64_h32_kv8_d128_traffic.txt"
 def parse_args(argv=None):
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--steps", type=int, default=500)
+    ap.add_argument("--warmup", type=int, default=400)
+    ap.add_argument("--prewarm-ms", type=float, default=100.0,
+                    help="untimed decode launches for at least this long before the warmup steps")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--sets", type=int, default=3, help="independent cache/query sets rotated per step")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="CPU baseline time budget")
@@ -197,6 +204,13 @@ def main(argv=None) -> int:
         torch.cuda.synchronize()
         print(f"calibration copy: {n} bytes read, {n} bytes written", file=sys.stderr)
 
+    prewarm = 0
+    t_pre = time.perf_counter()
+    while (time.perf_counter() - t_pre) * 1e3 < args.prewarm_ms:
+        for i in range(16):
+            _native.check(lib, fn(*argsets[i % args.sets]))
+        torch.cuda.synchronize()
+        prewarm += 16
     for i in range(args.warmup):
         _native.check(lib, fn(*argsets[i % args.sets]))
     torch.cuda.synchronize()
@@ -227,6 +241,7 @@ def main(argv=None) -> int:
         "n_gpus": 1,
         "steps": K,
         "warmup": args.warmup,
+        "prewarm": {"ms": args.prewarm_ms, "launches": prewarm},
         "ms_per_step": round(ms_per_step, 5),
         "us_per_step": round(ms_per_step * 1e3, 2),
         "pct_of_hbm_peak": round(100.0 * value / HBM_PEAK_GBS, 2),

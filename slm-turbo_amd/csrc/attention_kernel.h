@@ -258,16 +258,22 @@ __device__ void zero_empty(const AttnParams& p, int h0, int h1, int Weff) {
 
 // ZERO: zero the empty sequences' outputs here; otherwise the caller calls
 // zero_empty itself once it has a range (always done here when no workgroup
-// has tiles).
+// has tiles).  stash (LDS, optional): receives the lengths of sequences
+// 0 .. stash_n - 1, visible to the whole workgroup on return.
 template <int TT, int D, bool ZERO = true>
-__device__ bool schedule_range(const AttnParams& p, int* misc, int h0, int h1, TileRange& r) {
+__device__ bool schedule_range(const AttnParams& p, int* misc, int h0, int h1, TileRange& r, int* stash = nullptr,
+                               int stash_n = 0) {
   const int tid = threadIdx.x, lane = tid & 63, wave = uniform(tid >> 6);
   const int NT = blockDim.x, nwaves = NT >> 6;
   // exclusive scan of the per-sequence tile counts (threads own contiguous chunks)
   int my_excl, mysum = 0;
   const int chunk = (p.B + NT - 1) / NT;
   const int cb0 = min(p.B, tid * chunk), cb1 = min(p.B, cb0 + chunk);
-  for (int b = cb0; b < cb1; ++b) mysum += tiles_of<TT>(seq_len_lane(p, b));
+  for (int b = cb0; b < cb1; ++b) {
+    const int L = seq_len_lane(p, b);
+    if (b < stash_n) stash[b] = L;
+    mysum += tiles_of<TT>(L);
+  }
   {
     int v = mysum;
 #pragma unroll

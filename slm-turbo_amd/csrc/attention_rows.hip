@@ -79,7 +79,9 @@ struct Shape {
   static constexpr int QOFF = NS * STAGE;                 // one 1 KB query slot per wave
   static constexpr int WOFF = QOFF + WAVES * 1024;        // per-wave query-limb scratch
   static constexpr int MOFF = WOFF + WAVES * 1024;        // misc ints
-  static constexpr int LDS = MOFF + 32 * 4;
+  static constexpr int STASH = 256;                       // sequence lengths kept in LDS
+  static constexpr int SOFF = MOFF + 32 * 4;
+  static constexpr int LDS = SOFF + STASH * 4;
   static_assert(LDS <= 160 * 1024, "LDS ring too large");
 };
 
@@ -155,7 +157,8 @@ __global__ void __launch_bounds__(NKV * WPK * 64) rows_kernel(const AttnParams p
   uint8_t* const wscr = smem + S::WOFF + wave * 1024;
 
   TileRange rng;
-  if (!schedule_range<TT, D, false>(p, misc, h0, h1, rng)) return;
+  int* const stash = reinterpret_cast<int*>(smem + S::SOFF);
+  if (!schedule_range<TT, D, false>(p, misc, h0, h1, rng, stash, S::STASH)) return;
   const int lo = rng.lo, hi = rng.hi;
 
   // ---------------------------------------------------------------- loads
@@ -199,7 +202,8 @@ __global__ void __launch_bounds__(NKV * WPK * 64) rows_kernel(const AttnParams p
     int mb = -1, mtb = 0, mL = 0, mTb = 0;
     int b0 = cb, P0 = cP;
     for (;;) {
-      const int Ll = seq_len_lane(p, b0 + lane);   // 0 past the last sequence
+      const int bl = b0 + lane;
+      const int Ll = bl < S::STASH && bl < p.B ? stash[bl] : seq_len_lane(p, bl);   // 0 past the last sequence
       const int Tl = tiles_of<TT>(Ll);
       int incl = Tl;
 #pragma unroll
@@ -548,11 +552,14 @@ __global__ void __launch_bounds__(NKV * WPK * 64) rows_kernel(const AttnParams p
   // so waiting until NOPS operations remain covers tile t and its query.
   build(lo);
   int sinfo[2];
+  issue_q(rng.b);               // the query rows first: begin runs while tile lo flies
   sinfo[0] = issue(lo, 0);
-  issue_q(sinfo[0] >> 8);
   sinfo[1] = lo + 1 < hi ? issue(lo + 1, 1) : 0;
+  if (lo + 1 < hi) vm_wait_n<2 * S::NOPS>();
+  else vm_wait_n<S::NOPS>();
   int seg_first = lo;
-  bool seg_whole = false;
+  bool seg_whole = (sinfo[0] >> 7) & 1;
+  begin(*reinterpret_cast<const uint4*>(smem + S::QOFF + wave * 1024 + lane * 16));
   uint32_t xvs[2][2 * S::NP];   // V words of the tiles in the two stages
   uint32_t Ws[2][S::ROUNDS];    // their weights
   int pinfo = 0;                // info of the previous tile
@@ -569,7 +576,7 @@ __global__ void __launch_bounds__(NKV * WPK * 64) rows_kernel(const AttnParams p
     lds_barrier();
     const int info = sinfo[st];
     const bool first_of_seq = (info >> 7) & 1;
-    const bool seg_start = t == lo || first_of_seq;
+    const bool seg_start = t != lo && first_of_seq;   // the range's first segment began before the loop
     uint32_t kq[S::ROUNDS][4];
     uint2 kr[S::ROUNDS];
     read_tile(smem + st * S::STAGE + kvw * SLOT, kq, kr, xvs[st]);
