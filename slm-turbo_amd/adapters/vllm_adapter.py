@@ -17,6 +17,9 @@ Differences from the reference, on purpose:
   ``seq_lens`` and ``block_table`` directly (int32 tables are read as they
   are): no per-request loop, no ``.tolist()`` host sync, no int64 copies;
   the result is written straight into vLLM's output buffer;
+* a prefill chunk that continues cached context (the reference supports the
+  first chunk only) attends over the packed cache: every query token is one
+  sequence of the same batched launch (also one launch, no host sync);
 * the vLLM-independent logic lives in ``PackedKVAttentionMixin`` so it runs
   without vLLM (tests drive it with a fake ``attn_metadata`` carrying
   ``seq_lens``, ``block_table``, ``num_actual_tokens``, ``max_query_len`` --
@@ -116,8 +119,11 @@ class PackedKVAttentionMixin:
             return output.fill_(0)
         q = query[:N]
         if int(attn_metadata.max_query_len) > 1:
-            attn_out = self._prefill_attention(q, key[:N], value[:N], kv_cache, attn_metadata)
-            self._store_output(output, attn_out, N)
+            if self._has_context(attn_metadata):
+                self._chunked_attention(q, kv_cache, attn_metadata, output, N)
+            else:
+                attn_out = self._prefill_attention(q, key[:N], value[:N], kv_cache, attn_metadata)
+                self._store_output(output, attn_out, N)
         else:
             self._decode_attention(q, kv_cache, attn_metadata, output, N)
         return output
@@ -131,8 +137,9 @@ class PackedKVAttentionMixin:
 
     # ---- prefill: SDPA on the chunk's fp16 K/V (first chunk) ----------------
     def _prefill_attention(self, query, key, value, kv_cache, attn_metadata):
-        """Causal SDPA over the current chunk's raw K/V (reference :231-245);
-        chunked continuation over the packed cache is not supported."""
+        """Causal SDPA over the current chunk's raw K/V (reference :231-245),
+        for steps whose requests have no earlier context; a continuation
+        goes through _chunked_attention."""
         Hq, Hk = query.shape[1], key.shape[1]
         q_t = query.transpose(0, 1).unsqueeze(0)
         k_t = key.transpose(0, 1).unsqueeze(0)
@@ -141,18 +148,52 @@ class PackedKVAttentionMixin:
             q_t, k_t, v_t, is_causal=True, scale=self.scale, enable_gqa=Hk < Hq)
         return out[0].transpose(0, 1)
 
+    # ---- chunked prefill continuing cached context -------------------------
+    @staticmethod
+    def _has_context(attn_metadata) -> bool:
+        """True when some request of a multi-token step attends to tokens of
+        earlier steps: vLLM's host-side max_seq_len exceeds max_query_len."""
+        max_seq_len = getattr(attn_metadata, "max_seq_len", None)
+        if max_seq_len is None or getattr(attn_metadata, "query_start_loc", None) is None:
+            return False
+        return int(max_seq_len) > int(attn_metadata.max_query_len)
+
+    def _chunked_attention(self, query, kv_cache, attn_metadata, output, N):
+        """Prefill chunks that continue cached context, and any decode tokens
+        of the same step, over the packed cache (the reference leaves chunked
+        continuation unsupported, adapters/vllm_adapter.py:238-239).  Query
+        token i of request r sits at absolute position p = seq_len[r] -
+        query_len[r] + (i - query_start[r]) and attends to tokens [0, p] of r,
+        all of which this step's do_kv_cache_update has already written.  Each
+        query token becomes one sequence of length p + 1 with r's block-table
+        row: one batched launch, index arithmetic on the device, no host sync."""
+        qsl = attn_metadata.query_start_loc.to(torch.int64)       # [R+1]
+        R = qsl.numel() - 1
+        tok = torch.arange(N, device=query.device, dtype=torch.int64)
+        req = torch.searchsorted(qsl[1:].contiguous(), tok, right=True)   # request of each token
+        qlen = (qsl[1:] - qsl[:-1])[req]
+        seq = attn_metadata.seq_lens[:R].to(torch.int64)[req]
+        pos = seq - qlen + (tok - qsl[:-1][req])
+        tables = attn_metadata.block_table[:R][req]
+        self._paged_attention(query, kv_cache, (pos + 1).to(torch.int32), tables, output, N)
+
     # ---- decode: one batched launch over every request ----------------------
     def _decode_attention(self, query, kv_cache, attn_metadata, output, N):
         """query [N, H, D] (one token per request), kv_cache [nb, bs, KV, D+8]
         uint8; reads attn_metadata.seq_lens [N] and .block_table [N, max]
         on the device.  Writes output[:N]."""
+        self._paged_attention(query, kv_cache, attn_metadata.seq_lens[:N], attn_metadata.block_table[:N],
+                              output, N)
+
+    def _paged_attention(self, query, kv_cache, seq_lens, block_table, output, N):
+        """One batched paged decode launch: query row n attends to the first
+        seq_lens[n] tokens of block-table row n.  Writes output[:N] (in place
+        when the output buffer allows)."""
         global _KERNEL_CALLS
         kd = self._slm_kernels()
         block_size, num_kv_heads = kv_cache.shape[1], kv_cache.shape[2]
-        seq_lens = attn_metadata.seq_lens[:N]
         if seq_lens.dtype != torch.int32:
             seq_lens = seq_lens.to(torch.int32)
-        block_table = attn_metadata.block_table[:N]
         H, D = self.num_heads, self.head_size
         out3 = None
         if output.dtype in (torch.float16, torch.float32) and output.is_contiguous():

@@ -189,6 +189,47 @@ def test_prefill_routes_to_causal_sdpa_over_the_chunk():
     assert_close(out.reshape(N, H, D).numpy(), ref.numpy(), atol=1e-5, rtol=1e-5)
 
 
+def _chunk_meta(seq_lens, query_lens, block_table):
+    """A mixed step: request r has query_lens[r] new tokens and seq_lens[r]
+    tokens in total (the new ones included)."""
+    qsl = torch.zeros(len(query_lens) + 1, dtype=torch.int32)
+    qsl[1:] = torch.cumsum(torch.as_tensor(query_lens, dtype=torch.int32), 0)
+    return SimpleNamespace(seq_lens=torch.as_tensor(seq_lens, dtype=torch.int32),
+                           block_table=torch.as_tensor(block_table, dtype=torch.int32),
+                           query_start_loc=qsl, num_actual_tokens=int(qsl[-1]),
+                           max_query_len=max(query_lens), max_seq_len=max(seq_lens))
+
+
+def test_chunked_prefill_continuation_is_one_launch():
+    """A chunk continuing 20 cached tokens, a first chunk of 3 and a decode
+    token in one step: every query token becomes one sequence of the batched
+    launch, with its absolute position + 1 as length and its request's row."""
+    k = _RecordingKernels()
+    impl = _impl(kernels=k)
+    tables = torch.tensor([[4, 5], [6, 0], [7, 8]], dtype=torch.int32)
+    meta = _chunk_meta(seq_lens=[25, 3, 40], query_lens=[5, 3, 1], block_table=tables)
+    q = torch.randn(9, 8, 64).half()
+    out = torch.zeros(9, 512, dtype=torch.float16)
+    impl.forward(None, q, q, q, torch.zeros(9, 16, 2, 72, dtype=torch.uint8), meta, out)
+    assert len(k.decode_calls) == 1
+    c = k.decode_calls[0]
+    assert c["seq_lens"].tolist() == [21, 22, 23, 24, 25, 1, 2, 3, 40]
+    assert c["block_tables"].tolist() == [[4, 5]] * 5 + [[6, 0]] * 3 + [[7, 8]]
+    assert torch.all(out == 0.5)
+
+
+def test_first_chunks_keep_the_reference_prefill():
+    """Without earlier context the step keeps the reference's SDPA prefill."""
+    k = _RecordingKernels()
+    impl = _impl(kernels=k)
+    meta = _chunk_meta(seq_lens=[4, 3], query_lens=[4, 3], block_table=torch.zeros(2, 1, dtype=torch.int32))
+    q = torch.randn(7, 8, 64)
+    out = torch.zeros(7, 512)
+    impl.forward(None, q, q[:, :2], q[:, :2], torch.zeros(2, 16, 2, 72, dtype=torch.uint8), meta, out)
+    assert k.decode_calls == []
+    assert torch.all(torch.isfinite(out)) and not torch.all(out == 0)
+
+
 # ---------------------------------------------------------------- on the GPU
 @pytest.mark.gpu
 def test_backend_decode_matches_oracle_with_vllm_metadata():
@@ -223,3 +264,36 @@ def test_backend_store_is_bit_exact():
     impl.do_kv_cache_update(None, key.cuda(), val.cuda(), cache, slots.cuda())
     torch.cuda.synchronize()
     assert np.array_equal(cache.cpu().numpy(), ref)
+
+
+@pytest.mark.gpu
+def test_backend_chunked_prefill_matches_oracle():
+    """Real kernels: chunks of 7 and 12 tokens continuing 300 and 1000 cached
+    tokens, and one decode token, in one step; each query token against the
+    oracle over its own prefix of the packed cache."""
+    H, KV, D = 32, 8, 128
+    lens = [307, 1012, 90]
+    qlens = [7, 12, 1]
+    case = make_paged_case(seed=91, B=3, H=H, KV=KV, D=D, lens=lens)
+    N = sum(qlens)
+    g = torch.Generator().manual_seed(92)
+    q = torch.randn(N, H, D, generator=g).half()
+    # the oracle case: one sequence per query token
+    rows, vlens = [], []
+    for r, (L, n) in enumerate(zip(lens, qlens)):
+        for i in range(n):
+            rows.append(case.block_tables[r])
+            vlens.append(L - n + i + 1)
+    vcase = type(case)(q=q, kv_cache=case.kv_cache, block_tables=torch.stack(rows),
+                       seq_lens=torch.tensor(vlens, dtype=torch.int32), block_size=case.block_size,
+                       num_kv_heads=KV)
+    ref = paged_reference(vcase)
+    impl = _impl(H=H, D=D, KV=KV)
+    dev = "cuda:0"
+    meta = _chunk_meta(lens, qlens, case.block_tables)
+    for f in ("seq_lens", "block_table", "query_start_loc"):
+        setattr(meta, f, getattr(meta, f).to(dev))
+    out = torch.zeros(N, H * D, dtype=torch.float16, device=dev)
+    impl.forward(None, q.to(dev), q.to(dev), q.to(dev), torch.from_numpy(case.kv_cache).to(dev), meta, out)
+    torch.cuda.synchronize()
+    assert_close(out.float().cpu().numpy().reshape(N, H, D), ref, atol=3e-3, what="chunked prefill")
