@@ -109,3 +109,41 @@ def test_valu_roof_and_bound_selection():
     r8 = rl.decode_attention_bounds(lens, 64, 8, 128, dev)
     assert r8["valu_s"] == pytest.approx(2 * r["valu_s"])
     assert r8["bound"] == "valu" and r8["max_hbm_fraction"] < r["max_hbm_fraction"]
+
+
+# ---------------------------------------------------------------- device probe
+def test_device_probe_helpers():
+    import profiler
+    assert profiler.gfx_number("gfx950:sramecc+:xnack-") == 950
+    assert profiler.gfx_number("gfx942") == 942
+    assert profiler.gfx_number("") == 0
+    assert profiler.bandwidth_of("gfx950:sramecc+:xnack-") == 8000.0
+    assert profiler.bandwidth_of("gfx942") == 5300.0
+
+
+def test_packed_kv_bytes_per_token():
+    """Llama-1.1B-shaped (22 layers, 4 KV heads, head_dim 64): 72-byte packed
+    slot per KV head and layer against 2 x 64 x 2 bytes of fp16 K and V."""
+    import profiler
+    assert profiler.kv_cache_bytes_per_token(4, 64, 22) == 22 * 4 * 72
+    assert profiler.kv_cache_bytes_per_token(4, 64, 22, packed=False) == 2 * 4 * 64 * 22 * 2
+    assert profiler.kv_cache_bytes_per_token(8, 128, 1) == 8 * 136     # one cache row of the decode
+
+
+def test_device_info_without_a_gpu_raises():
+    import torch
+    import profiler
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is present")
+    with pytest.raises(RuntimeError, match="No CUDA device available"):
+        profiler.device_info(0)
+
+
+@pytest.mark.gpu
+def test_device_info_on_the_gpu():
+    import profiler
+    d = profiler.device_info(0)
+    assert d.sm_version == 950 and d.sm_count >= 256
+    assert d.memory_bandwidth_gbps == 8000.0
+    assert d.vram_mb > 250 * 1024
+    assert d.supports_tensor_cores and d.supports_async_copy
