@@ -4,6 +4,8 @@
   / 8 KV heads, head_dim 128, block 16, K/V ~ N(0, 1).
 * The long-context configuration: batch 8, lengths U[32768, 131072], 64 query /
   8 KV heads, head_dim 128, block 16, K/V ~ Student-t(3).
+* The full-model workload's attention: batch 32, lengths U[4096, 4224], 32
+  query / 4 KV heads, head_dim 64, block 16.
 
 Caches are filled on the device by the store kernel, block tables are a random
 permutation of exactly the blocks needed.  At these sizes the float64 oracle
@@ -126,3 +128,14 @@ def test_long_context_configuration_full_size():
         tables2[b, n:] = 0
     got2 = decode(q, moved, tables2, lens, KV)
     assert torch.equal(got, got2)
+
+
+def test_full_model_attention_shape():
+    """The full-model workload's decode: batch 32, 32 query / 4 KV heads,
+    head_dim 64, lengths U[4096, 4224] (a 4096-token prompt plus up to 128
+    generated tokens)."""
+    B, H, KV, D = 32, 32, 4, 64
+    lens, tables, q, cache = build(0, B, H, KV, D, 4096, 4224, "normal")
+    got = decode(q, cache, tables, lens, KV)
+    ref = reference(q, cache, tables, lens, KV)
+    assert_close(got.cpu().numpy(), ref.cpu().numpy(), what="batch 32, H=32 KV=4 D=64, U[4096,4224]")
