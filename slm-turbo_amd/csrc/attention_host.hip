@@ -75,8 +75,8 @@ int plan_attention(int B, int H, int G, int D, int dma_kv, AttnPlan* plan) {
   plan->rows_nkv = plan->rows_wpk = plan->rows_groups = 0;
   if (dma_kv <= 0) return SLMT_OK;
 
-  // Whole-row kernel first: it covers head_dim 128 with 4 or 8 query heads per
-  // KV head.  The workspace is sized for the larger of its grid and the
+  // Whole-row kernel first: it covers head_dim 64 and 128 with 4 or 8 query
+  // heads per KV head.  The workspace is sized for the larger of its grid and the
   // other plans' (W_ws).
   int nkv, wpk, rgroups;
   if (rows_shape(H, G, D, dma_kv, &nkv, &wpk, &rgroups)) {
@@ -84,7 +84,7 @@ int plan_attention(int B, int H, int G, int D, int dma_kv, AttnPlan* plan) {
     plan->rows_nkv = nkv;
     plan->rows_wpk = wpk;
     plan->rows_groups = rgroups;
-    plan->W_ws = std::max(plan->W_ws, rows_max_workgroups(nkv, wpk, rgroups, cus));
+    plan->W_ws = std::max(plan->W_ws, rows_max_workgroups(D, nkv, wpk, rgroups, cus));
   }
 
   // Direct-load plan: every wave's 4 heads share one KV head (G % 4 == 0) and
@@ -102,7 +102,7 @@ int plan_attention(int B, int H, int G, int D, int dma_kv, AttnPlan* plan) {
   plan->dma = true;
   plan->lds_bytes = (size_t)geo.total;
   if (plan->W > plan->W_ws) plan->W_ws = plan->W;
-  if (plan->rows) plan->W_ws = std::max(plan->W_ws, rows_max_workgroups(nkv, wpk, rgroups, cus));
+  if (plan->rows) plan->W_ws = std::max(plan->W_ws, rows_max_workgroups(D, nkv, wpk, rgroups, cus));
   return SLMT_OK;
 }
 
@@ -147,7 +147,7 @@ int launch_attention(int mode, int D, AttnParams& p, void* workspace, int64_t ws
   if (p.min_tiles <= 0) p.min_tiles = 4;
   if (mode == SRC_PAGED && pl.rows) {
     p.W = pl.W_ws;   // the kernel lowers it to the workgroups the CUs hold
-    return launch_attention_rows(pl.rows_nkv, pl.rows_wpk, pl.rows_groups, p, stream);
+    return launch_attention_rows(D, pl.rows_nkv, pl.rows_wpk, pl.rows_groups, p, stream);
   }
   const dim3 grid(pl.W, pl.groups), block(pl.waves * 64);
   if (mode == SRC_PAGED) {

@@ -1,10 +1,10 @@
-// Batched paged 4-bit decode attention for head_dim 128 with 4 or 8 query
-// heads per KV head: the "whole-row" kernel (reference kernel it replaces:
+// Batched paged 4-bit decode attention for head_dim 64 or 128 with 4 or 8
+// query heads per KV head: the "whole-row" kernel (reference kernel it replaces:
 // kv_dequant_decode_per_token_paged_kernel, kernels/kv_dequant_kernels.cuh:671-801,
 // batched over the whole decode step instead of launched per request).
 //
 // A workgroup owns NKV consecutive KV heads (a 16-byte aligned sub-row of every
-// cache row, NKV * 136 bytes) and their 4*WPK query heads each, one wave per 4
+// cache row, NKV * (D + 8) bytes) and their 4*WPK query heads each, one wave per 4
 // query heads.  Tiles are TT tokens (64, or 32 where a wave's share of a
 // 64-token tile would cross a paged block).  Work is split stream-K over the
 // concatenated tile list of all sequences, exactly as in attention_kernel.h,
@@ -56,12 +56,13 @@ namespace rows {
 
 using namespace attn;
 
-constexpr int D = 128, SLOT = D + 8;
-
-template <int NKV, int WPK, int TT>
+template <int D, int NKV, int WPK, int TT>
 struct Shape {
+  static_assert(D == 64 || D == 128, "head_dim 64 or 128");
   static_assert(NKV % 2 == 0, "sub-rows must be a whole number of 16-byte units");
   static_assert(TT % 16 == 0, "tiles of whole QK rounds");
+  static constexpr int SLOT = D + 8;            // bytes of one KV head in a cache row
+  static constexpr int DQ = D / 32;             // key dwords per QK quarter = V bytes per PV lane
   static constexpr int NS = 2;                  // LDS ring stages
   static constexpr int WAVES = NKV * WPK;
   static constexpr int THREADS = WAVES * 64;
@@ -85,7 +86,9 @@ struct Shape {
   static_assert(LDS <= 160 * 1024, "LDS ring too large");
 };
 
-constexpr float kC = 1.4426950408889634f / 11.313708498984761f;   // log2(e) / sqrt(128)
+// log2(e) / sqrt(D)
+template <int D>
+constexpr float kC = D == 128 ? 1.4426950408889634f / 11.313708498984761f : 1.4426950408889634f / 8.0f;
 
 // One token pair's PV products: al[k][h] += dot(w of lane 8*I + h of this
 // row, lo[k]) and af[k][h] += dot(that w, fu[k]) for bytes k and heads h, 32
@@ -133,15 +136,52 @@ __device__ __forceinline__ void pv_pair_bcast(float (&al)[4][4], float (&af)[4][
         "n"(8 * I), "n"(8 * I + 1), "n"(8 * I + 2), "n"(8 * I + 3));
 }
 
+// The same for head_dim 64, where a PV lane holds 2 V bytes per token: 16
+// products.
+template <int I>
+__device__ __forceinline__ void pv_pair_bcast(float (&al)[2][4], float (&af)[2][4], uint32_t w, const uint32_t (&lo)[2],
+                                              const uint32_t (&fu)[2]) {
+  asm("s_nop 1\n\t"
+      "v_dot2c_f32_f16_dpp %0, %16, %17 row_newbcast:%21 row_mask:0xf bank_mask:0xf\n\t"
+      "v_dot2c_f32_f16_dpp %8, %16, %19 row_newbcast:%21 row_mask:0xf bank_mask:0xf\n\t"
+      "v_dot2c_f32_f16_dpp %4, %16, %18 row_newbcast:%21 row_mask:0xf bank_mask:0xf\n\t"
+      "v_dot2c_f32_f16_dpp %12, %16, %20 row_newbcast:%21 row_mask:0xf bank_mask:0xf\n\t"
+      "v_dot2c_f32_f16_dpp %1, %16, %17 row_newbcast:%22 row_mask:0xf bank_mask:0xf\n\t"
+      "v_dot2c_f32_f16_dpp %9, %16, %19 row_newbcast:%22 row_mask:0xf bank_mask:0xf\n\t"
+      "v_dot2c_f32_f16_dpp %5, %16, %18 row_newbcast:%22 row_mask:0xf bank_mask:0xf\n\t"
+      "v_dot2c_f32_f16_dpp %13, %16, %20 row_newbcast:%22 row_mask:0xf bank_mask:0xf\n\t"
+      "v_dot2c_f32_f16_dpp %2, %16, %17 row_newbcast:%23 row_mask:0xf bank_mask:0xf\n\t"
+      "v_dot2c_f32_f16_dpp %10, %16, %19 row_newbcast:%23 row_mask:0xf bank_mask:0xf\n\t"
+      "v_dot2c_f32_f16_dpp %6, %16, %18 row_newbcast:%23 row_mask:0xf bank_mask:0xf\n\t"
+      "v_dot2c_f32_f16_dpp %14, %16, %20 row_newbcast:%23 row_mask:0xf bank_mask:0xf\n\t"
+      "v_dot2c_f32_f16_dpp %3, %16, %17 row_newbcast:%24 row_mask:0xf bank_mask:0xf\n\t"
+      "v_dot2c_f32_f16_dpp %11, %16, %19 row_newbcast:%24 row_mask:0xf bank_mask:0xf\n\t"
+      "v_dot2c_f32_f16_dpp %7, %16, %18 row_newbcast:%24 row_mask:0xf bank_mask:0xf\n\t"
+      "v_dot2c_f32_f16_dpp %15, %16, %20 row_newbcast:%24 row_mask:0xf bank_mask:0xf"
+      : "+v"(al[0][0]), "+v"(al[0][1]), "+v"(al[0][2]), "+v"(al[0][3]), "+v"(al[1][0]), "+v"(al[1][1]), "+v"(al[1][2]), "+v"(al[1][3]), "+v"(af[0][0]), "+v"(af[0][1]), "+v"(af[0][2]), "+v"(af[0][3]), "+v"(af[1][0]), "+v"(af[1][1]), "+v"(af[1][2]), "+v"(af[1][3])
+      : "v"(w), "v"(lo[0]), "v"(lo[1]), "v"(fu[0]), "v"(fu[1]),
+        "n"(8 * I), "n"(8 * I + 1), "n"(8 * I + 2), "n"(8 * I + 3));
+}
+
+// Sum of x over the 4 rows of 16 lanes (lanes l, l + 16, l + 32, l + 48).
+__device__ __forceinline__ float rows_sum(float x) {
+  float a, b;
+  swap16(x, a, b);
+  x = a + b;
+  swap32(x, a, b);
+  return a + b;
+}
+
 // x *= s in x's own register: a conditionally rescaled accumulator then stays
 // in one register on both paths of the branch (no copies on the common path).
 __device__ __forceinline__ void scale_in_place(float& x, float s) {
   asm volatile("v_mul_f32 %0, %1, %0" : "+v"(x) : "s"(s));
 }
 
-template <int NKV, int WPK, int TT>
+template <int D, int NKV, int WPK, int TT>
 __global__ void __launch_bounds__(NKV * WPK * 64) rows_kernel(const AttnParams p) {
-  using S = Shape<NKV, WPK, TT>;
+  using S = Shape<D, NKV, WPK, TT>;
+  constexpr int SLOT = S::SLOT, DQ = S::DQ;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
 
   const int tid = threadIdx.x;
@@ -179,9 +219,11 @@ __global__ void __launch_bounds__(NKV * WPK * 64) rows_kernel(const AttnParams p
   }
   const uint32_t lds_smem = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)smem;
   const uint32_t lds_run = lds_smem + rw0 * S::RSTRIDE;
-  // query rows: lane (qp, qg) moves dims 8qp .. 8qp+7 of head hw + qg
+  // query rows: lane (qp, qg) moves dims 8qp .. 8qp+7 of head hw + qg (head_dim
+  // 64: lanes qp >= 8 re-read dims 8(qp - 8) .., which begin() ignores)
   const int qp = lane >> 2, qg = lane & 3;
-  const uint32_t qoff = (uint32_t)(((hw + qg) * p.q_head_stride + qp * 8) * 2);
+  const int qd = D == 128 ? qp : (qp & 7);
+  const uint32_t qoff = (uint32_t)(((hw + qg) * p.q_head_stride + qd * 8) * 2);
 
   // Tile descriptors, 64 tiles at a time, lane i for tile dchunk + i: the
   // address of this wave's first row and an info word
@@ -278,32 +320,33 @@ __global__ void __launch_bounds__(NKV * WPK * 64) rows_kernel(const AttnParams p
 
   // ---------------------------------------------------------------- per-wave state
   // QK lane (token p, key quarter qc = lane & 3): limbs of all 4 heads for
-  // the lane's 4 key dwords, in the order the lane reads them (odd quarters
-  // read their two 8-byte halves swapped, so the quad covers all 32 banks).
-  // Heads are stored rotated: slot j holds head (qc + j) & 3, so the quad's
-  // reduce-scatter needs no per-lane selects.
-  uint32_t qlq[4][4][4];              // [head slot][dword][limb]
+  // the lane's DQ key dwords, in the order the lane reads them (head_dim 128:
+  // odd quarters read their two 8-byte halves swapped, so the quad covers all
+  // 32 banks).  Heads are stored rotated: slot j holds head (qc + j) & 3, so
+  // the quad's reduce-scatter needs no per-lane selects.
+  uint32_t qlq[4][DQ][4];             // [head slot][dword][limb]
   // Scores are kept in query-integer units, u = step * (qi . n) + min * sum(qi);
   // qa converts them to base-2 logits (log2(e) / sqrt(D) / query scale), so a
   // weight is exp2((u - m_run) * qa) and m_run is the running max of u.
   float qa = 0.f, qb = 0.f, mq = 0.f, m_run = -INFINITY, l_run = 0.f, vmt = 0.f;
-  float accl[4][4], accf[4][4];       // [byte k][head]: sum w * lo, sum w * (lo + 16 hi), units of 2^-24
-  const int pc = lane & 15, pq = lane >> 4;   // PV: dword column, token group
+  float accl[DQ][4], accf[DQ][4];     // [byte k][head]: sum w * lo, sum w * (lo + 16 hi), units of 2^-24
+  const int pc = lane & 15, pq = lane >> 4;   // PV: V column (DQ bytes), token group
 
   auto begin = [&](const uint4 w) {
     m_run = -INFINITY;
     l_run = 0.f;
     vmt = 0.f;
 #pragma unroll
-    for (int k = 0; k < 4; ++k)
+    for (int k = 0; k < DQ; ++k)
 #pragma unroll
       for (int h = 0; h < 4; ++h) accl[k][h] = accf[k][h] = 0.f;
     const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+    const bool qlive = D == 128 || qp < 8;
     float qv[8];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      qv[2 * i] = h2f((uint16_t)(ws[i] & 0xffffu));
-      qv[2 * i + 1] = h2f((uint16_t)(ws[i] >> 16));
+      qv[2 * i] = qlive ? h2f((uint16_t)(ws[i] & 0xffffu)) : 0.f;
+      qv[2 * i + 1] = qlive ? h2f((uint16_t)(ws[i] >> 16)) : 0.f;
     }
     float amax = 0.f;
 #pragma unroll
@@ -331,20 +374,26 @@ __global__ void __launch_bounds__(NKV * WPK * 64) rows_kernel(const AttnParams p
 #pragma unroll
     for (int k = 0; k < 4; ++k) wl[(qg * 4 + k) * 16 + qp] = limb[k];
     wave_lds_sync();
-    // (head h, limb k) words 4qc .. 4qc+3 of this lane's quarter
+    // (head h, limb k) words DQ*qc .. DQ*qc+DQ-1 of this lane's quarter
     const bool swp = qg & 1;
 #pragma unroll
     for (int j = 0; j < 4; ++j)
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
         const int h = (qg + j) & 3;
-        const uint4 v = *reinterpret_cast<const uint4*>(wl + (h * 4 + k) * 16 + 4 * qg);
-        qlq[j][0][k] = swp ? v.z : v.x;
-        qlq[j][1][k] = swp ? v.w : v.y;
-        qlq[j][2][k] = swp ? v.x : v.z;
-        qlq[j][3][k] = swp ? v.y : v.w;
+        if constexpr (D == 128) {
+          const uint4 v = *reinterpret_cast<const uint4*>(wl + (h * 4 + k) * 16 + 4 * qg);
+          qlq[j][0][k] = swp ? v.z : v.x;
+          qlq[j][1][k] = swp ? v.w : v.y;
+          qlq[j][2][k] = swp ? v.x : v.z;
+          qlq[j][3][k] = swp ? v.y : v.w;
+        } else {
+          const uint2 v = *reinterpret_cast<const uint2*>(wl + (h * 4 + k) * 16 + 2 * qg);
+          qlq[j][0][k] = v.x;
+          qlq[j][1][k] = v.y;
+        }
       }
-    qa = kC * rsq;
+    qa = kC<D> * rsq;
     qb = qsum;
   };
 
@@ -353,7 +402,7 @@ __global__ void __launch_bounds__(NKV * WPK * 64) rows_kernel(const AttnParams p
   // accumulator is shifted by 4 bits between limbs), then the quad's partial
   // dots for head qg gathered from the rotated slots with three DPP adds;
   // kr: the token's rulers.
-  auto score = [&](const uint32_t (&kq)[4], uint2 kr) -> float {
+  auto score = [&](const uint32_t (&kq)[DQ], uint2 kr) -> float {
     uint32_t part[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -362,14 +411,14 @@ __global__ void __launch_bounds__(NKV * WPK * 64) rows_kernel(const AttnParams p
       for (int k = 3; k >= 0; --k) {
         if (k < 3) x <<= 4;
 #pragma unroll
-        for (int d = 0; d < 4; ++d) x = __builtin_amdgcn_udot8(kq[d], qlq[j][d][k], x, false);
+        for (int d = 0; d < DQ; ++d) x = __builtin_amdgcn_udot8(kq[d], qlq[j][d][k], x, false);
       }
       part[j] = x;
     }
     // nibble sum of the token: the quad's quarters
     uint32_t sn = 0;
 #pragma unroll
-    for (int d = 0; d < 4; ++d) sn = __builtin_amdgcn_udot8(kq[d], 0x11111111u, sn, false);
+    for (int d = 0; d < DQ; ++d) sn = __builtin_amdgcn_udot8(kq[d], 0x11111111u, sn, false);
     // (the empty asm keeps each DPP move next to a two-operand add, which the
     // backend then fuses into one v_add_u32_dpp)
     sn += dpp_u<DPP_QUAD_XOR1>(sn);
@@ -393,26 +442,37 @@ __global__ void __launch_bounds__(NKV * WPK * 64) rows_kernel(const AttnParams p
 
   // LDS reads of tile data for this lane: its key quarter and rulers of its
   // QK tokens, and its V words (PV, used one iteration later).
-  auto read_tile = [&](const uint8_t* Sb, uint32_t (&kq)[S::ROUNDS][4], uint2 (&kr)[S::ROUNDS],
+  auto read_tile = [&](const uint8_t* Sb, uint32_t (&kq)[S::ROUNDS][DQ], uint2 (&kr)[S::ROUNDS],
                        uint32_t (&xv)[2 * S::NP]) {
     const int sw = (qg & 1) * 8;
 #pragma unroll
     for (int r = 0; r < S::ROUNDS; ++r) {
       const uint8_t* kb = Sb + (16 * r + qp) * S::RSTRIDE;
-      const uint2 k01 = *reinterpret_cast<const uint2*>(kb + 16 * qg + sw);
-      const uint2 k23 = *reinterpret_cast<const uint2*>(kb + 16 * qg + 8 - sw);
-      kq[r][0] = k01.x;
-      kq[r][1] = k01.y;
-      kq[r][2] = k23.x;
-      kq[r][3] = k23.y;
+      if constexpr (D == 128) {
+        const uint2 k01 = *reinterpret_cast<const uint2*>(kb + 16 * qg + sw);
+        const uint2 k23 = *reinterpret_cast<const uint2*>(kb + 16 * qg + 8 - sw);
+        kq[r][0] = k01.x;
+        kq[r][1] = k01.y;
+        kq[r][2] = k23.x;
+        kq[r][3] = k23.y;
+      } else {
+        const uint2 k01 = *reinterpret_cast<const uint2*>(kb + 8 * qg);
+        kq[r][0] = k01.x;
+        kq[r][1] = k01.y;
+      }
       kr[r] = *reinterpret_cast<const uint2*>(kb + D);
     }
-    const uint8_t* vb = Sb + D / 2 + 4 * pc;
+    const uint8_t* vb = Sb + D / 2 + DQ * pc;
 #pragma unroll
     for (int j = 0; j < S::NP; ++j) {
       const int P = pair_of(j);
-      xv[2 * j] = *reinterpret_cast<const uint32_t*>(vb + (2 * P) * S::RSTRIDE);
-      xv[2 * j + 1] = *reinterpret_cast<const uint32_t*>(vb + (2 * P + 1) * S::RSTRIDE);
+      if constexpr (D == 128) {
+        xv[2 * j] = *reinterpret_cast<const uint32_t*>(vb + (2 * P) * S::RSTRIDE);
+        xv[2 * j + 1] = *reinterpret_cast<const uint32_t*>(vb + (2 * P + 1) * S::RSTRIDE);
+      } else {
+        xv[2 * j] = *reinterpret_cast<const uint16_t*>(vb + (2 * P) * S::RSTRIDE);
+        xv[2 * j + 1] = *reinterpret_cast<const uint16_t*>(vb + (2 * P + 1) * S::RSTRIDE);
+      }
     }
   };
 
@@ -420,7 +480,7 @@ __global__ void __launch_bounds__(NKV * WPK * 64) rows_kernel(const AttnParams p
   // W[r] of the lane of (token 16r + qp, head qg) with qp even holds the fp16
   // pair (w(token), w(token + 1)) of head qg.  Tokens past the sequence end
   // get u = -inf, hence weight exp2(-inf) = 0.
-  auto qk_softmax = [&](const uint32_t (&kq)[S::ROUNDS][4], const uint2 (&kr)[S::ROUNDS], int nvalid,
+  auto qk_softmax = [&](const uint32_t (&kq)[S::ROUNDS][DQ], const uint2 (&kr)[S::ROUNDS], int nvalid,
                         uint32_t (&W)[S::ROUNDS]) {
     float s2[S::ROUNDS];
 #pragma unroll
@@ -444,7 +504,7 @@ __global__ void __launch_bounds__(NKV * WPK * 64) rows_kernel(const AttnParams p
       for (int h = 0; h < 4; ++h) {
         const float ah = readlane_f(alpha, h);
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
+        for (int k = 0; k < DQ; ++k) {
           scale_in_place(accl[k][h], ah);
           scale_in_place(accf[k][h], ah);
         }
@@ -472,9 +532,9 @@ __global__ void __launch_bounds__(NKV * WPK * 64) rows_kernel(const AttnParams p
 #pragma unroll
     for (int j = 0; j < S::NP; ++j) {
       const uint32_t x0 = xv[2 * j], x1 = xv[2 * j + 1];
-      uint32_t lo[4], fu[4];
+      uint32_t lo[DQ], fu[DQ];
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
+      for (int k = 0; k < DQ; ++k) {
         // byte k of both tokens at bits 0-7 and 16-23
         fu[k] = __builtin_amdgcn_perm(x1, x0, 0x0C000C00u | ((4u + k) << 16) | (uint32_t)k);
         lo[k] = fu[k] & 0x000F000Fu;
@@ -490,6 +550,52 @@ __global__ void __launch_bounds__(NKV * WPK * 64) rows_kernel(const AttnParams p
   auto finish = [&](int b, int seg_first, bool whole, bool last_of_seq) {
     const float lt = red16_sum(l_run);   // lane g: head g
     const float vt = red16_sum(vmt);
+    if constexpr (D == 64) {
+      // Every accumulator summed over the 4 token groups (rows) in every lane;
+      // lane (pc, row pq) then writes byte pq & 1 of its column (dims 4pc +
+      // 2(pq & 1), +1) for heads 2(pq >> 1) and 2(pq >> 1) + 1.
+      const int kb = pq & 1, hp = pq >> 1;
+      float o[2][2];                     // [head 2hp + i][dim]
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        float lo_t[2], fu_t[2], vh[2];
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+          const int h = 2 * hh + i;
+          const float l0 = rows_sum(accl[0][h]), l1 = rows_sum(accl[1][h]);
+          const float f0 = rows_sum(accf[0][h]), f1 = rows_sum(accf[1][h]);
+          lo_t[hh] = kb ? l1 : l0;
+          fu_t[hh] = kb ? f1 : f0;
+          vh[hh] = readlane_f(vt, h);
+        }
+        const float lsel = hp ? lo_t[1] : lo_t[0], fsel = hp ? fu_t[1] : fu_t[0], vsel = hp ? vh[1] : vh[0];
+        o[i][0] = lsel * 16777216.0f + vsel;             // 2^24: nibble-as-subnormal scale
+        o[i][1] = (fsel - lsel) * 1048576.0f + vsel;     // (16 hi) * 2^-24 -> hi
+      }
+      const int dcol = 4 * pc + 2 * kb;
+      if (whole && last_of_seq) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          const float l0 = readlane_f(lt, i), l2 = readlane_f(lt, 2 + i);
+          const float rL = __builtin_amdgcn_rcpf(hp ? l2 : l0);
+          const int h = 2 * hp + i;
+          const int64_t off = (int64_t)b * p.out_seq_stride + (int64_t)(hw + h) * p.out_head_stride + dcol;
+          if (p.out_f16) {
+            *reinterpret_cast<uint32_t*>(reinterpret_cast<uint16_t*>(p.out) + off) =
+                (uint32_t)f2h(o[i][0] * rL) | ((uint32_t)f2h(o[i][1] * rL) << 16);
+          } else {
+            *reinterpret_cast<float2*>(reinterpret_cast<float*>(p.out) + off) = make_float2(o[i][0] * rL, o[i][1] * rL);
+          }
+        }
+      } else {
+        const int slot = (seg_first == lo) ? 0 : 1;
+        const int64_t pbase = ((int64_t)wg * 2 + slot) * p.H;
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+          store_pair_agent(p.part_o + (pbase + hw + 2 * hp + i) * D + dcol, o[i][0], o[i][1]);
+        if (lane < 4) store_pair_agent(p.part_ml + (pbase + hw + lane) * 2, m_run * qa, lt);
+      }
+    } else {
     // Sum every accumulator over the 4 token groups (rows of 16 lanes).  The
     // four values (head h, lo|full, byte k = 0..3) are folded together: two
     // permlane16 swaps and one permlane32 swap leave the total of byte k in
@@ -534,6 +640,7 @@ __global__ void __launch_bounds__(NKV * WPK * 64) rows_kernel(const AttnParams p
       // lane g: head g; the running max in base-2 logits
       if (lane < 4) store_pair_agent(p.part_ml + (pbase + hw + lane) * 2, m_run * qa, lt);
     }
+    }
   };
 
   // ---------------------------------------------------------------- pipeline
@@ -577,7 +684,7 @@ __global__ void __launch_bounds__(NKV * WPK * 64) rows_kernel(const AttnParams p
     const int info = sinfo[st];
     const bool first_of_seq = (info >> 7) & 1;
     const bool seg_start = t != lo && first_of_seq;   // the range's first segment began before the loop
-    uint32_t kq[S::ROUNDS][4];
+    uint32_t kq[S::ROUNDS][DQ];
     uint2 kr[S::ROUNDS];
     read_tile(smem + st * S::STAGE + kvw * SLOT, kq, kr, xvs[st]);
     uint4 qw = make_uint4(0u, 0u, 0u, 0u);
@@ -633,7 +740,7 @@ __global__ void __launch_bounds__(NKV * WPK * 64) rows_kernel(const AttnParams p
 // Empty sequences get zeros here.  The decode kernel's partial stores are
 // visible because this kernel runs after it on the same stream.
 constexpr int MH = 8;   // heads per merge workgroup
-template <int TT>
+template <int D, int TT>
 __global__ void __launch_bounds__(128) merge_kernel(const AttnParams p) {
   const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int h0 = blockIdx.y * MH, h1 = min(p.H, h0 + MH);
@@ -687,10 +794,10 @@ static int blocks_per_cu(const void* kern, int threads, size_t lds) {
   return n;
 }
 
-template <int NKV, int WPK, int TT>
+template <int D, int NKV, int WPK, int TT>
 static int launch(AttnParams p, int groups, hipStream_t stream) {
-  using S = Shape<NKV, WPK, TT>;
-  auto kern = rows_kernel<NKV, WPK, TT>;
+  using S = Shape<D, NKV, WPK, TT>;
+  auto kern = rows_kernel<D, NKV, WPK, TT>;
   const int per_cu = blocks_per_cu(reinterpret_cast<const void*>(kern), S::THREADS, S::LDS);
   const int cus = device_cu_count();
   int W = std::max(1, cus * std::max(1, per_cu) / groups);
@@ -701,7 +808,7 @@ static int launch(AttnParams p, int groups, hipStream_t stream) {
   hipLaunchKernelGGL(kern, dim3(W, groups), dim3(S::THREADS), S::LDS, stream, p);
   if (int rc = check_launch("paged decode")) return rc;
   if (p.B > 0) {
-    hipLaunchKernelGGL(merge_kernel<TT>, dim3(p.B, (p.H + MH - 1) / MH), dim3(128), 0, stream, p);
+    hipLaunchKernelGGL((merge_kernel<D, TT>), dim3(p.B, (p.H + MH - 1) / MH), dim3(128), 0, stream, p);
     return check_launch("paged decode merge");
   }
   return 0;
@@ -711,7 +818,7 @@ static int launch(AttnParams p, int groups, hipStream_t stream) {
 
 // Shape of the whole-row kernel for a request, or false if it does not apply.
 bool rows_shape(int H, int G, int D, int cache_kv, int* nkv, int* wpk, int* groups) {
-  if (D != rows::D || (G != 4 && G != 8) || H % G != 0) return false;
+  if ((D != 64 && D != 128) || (G != 4 && G != 8) || H % G != 0) return false;
   const int KV = H / G;
   if (cache_kv != KV || cache_kv % 2 != 0) return false;
   const int w = G / 4;
@@ -725,18 +832,21 @@ bool rows_shape(int H, int G, int D, int cache_kv, int* nkv, int* wpk, int* grou
   return true;
 }
 
-// Instantiations (KV heads per workgroup, waves per KV head, tokens per
-// tile): 64-token tiles where a wave's rows fit one 16-row block, 32-token
+// Instantiations (head_dim, KV heads per workgroup, waves per KV head, tokens
+// per tile): 64-token tiles where a wave's rows fit one 16-row block, 32-token
 // tiles otherwise.
-#define SLMT_ROWS_CONFIGS(X) X(8, 1, 64) X(4, 1, 64) X(2, 1, 32) X(4, 2, 64) X(2, 2, 64)
+#define SLMT_ROWS_CONFIGS(X)                                                                 \
+  X(128, 8, 1, 64) X(128, 4, 1, 64) X(128, 2, 1, 32) X(128, 4, 2, 64) X(128, 2, 2, 64)     \
+  X(64, 8, 1, 64) X(64, 4, 1, 64) X(64, 2, 1, 32) X(64, 4, 2, 64) X(64, 2, 2, 64)
+#define SLMT_ROWS_KEY(d, a, b) ((d) * 100 + (a) * 10 + (b))
 
 // Workgroups per head group the whole-row kernel may use (its workspace bound).
-int rows_max_workgroups(int nkv, int wpk, int groups, int cus) {
+int rows_max_workgroups(int D, int nkv, int wpk, int groups, int cus) {
   const int waves = nkv * wpk;
   // at most 8 waves per CU (up to 256 VGPRs each), and the ring's LDS
   size_t lds = 0;
-  switch (nkv * 10 + wpk) {
-#define SLMT_ROWS_LDS(a, b, c) case a * 10 + b: lds = rows::Shape<a, b, c>::LDS; break;
+  switch (SLMT_ROWS_KEY(D, nkv, wpk)) {
+#define SLMT_ROWS_LDS(d, a, b, c) case SLMT_ROWS_KEY(d, a, b): lds = rows::Shape<d, a, b, c>::LDS; break;
     SLMT_ROWS_CONFIGS(SLMT_ROWS_LDS)
 #undef SLMT_ROWS_LDS
     default: return 1;
@@ -746,9 +856,9 @@ int rows_max_workgroups(int nkv, int wpk, int groups, int cus) {
   return std::max(1, cus * per_cu / groups);
 }
 
-int launch_attention_rows(int nkv, int wpk, int groups, const AttnParams& p, hipStream_t stream) {
-  switch (nkv * 10 + wpk) {
-#define SLMT_ROWS_LAUNCH(a, b, c) case a * 10 + b: return rows::launch<a, b, c>(p, groups, stream);
+int launch_attention_rows(int D, int nkv, int wpk, int groups, const AttnParams& p, hipStream_t stream) {
+  switch (SLMT_ROWS_KEY(D, nkv, wpk)) {
+#define SLMT_ROWS_LAUNCH(d, a, b, c) case SLMT_ROWS_KEY(d, a, b): return rows::launch<d, a, b, c>(p, groups, stream);
     SLMT_ROWS_CONFIGS(SLMT_ROWS_LAUNCH)
 #undef SLMT_ROWS_LAUNCH
     default: return fail(SLMT_ERR_INVALID, "paged decode: no whole-row kernel for this shape");

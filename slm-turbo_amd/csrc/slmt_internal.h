@@ -215,8 +215,8 @@ int plan_attention(int B, int H, int G, int D, int dma_kv, AttnPlan* plan);
 // Whole-row kernel (attention_rows.hip): its shape for a request (false if it
 // does not apply), the workgroups per head group it may use, and its launch.
 bool rows_shape(int H, int G, int D, int cache_kv, int* nkv, int* wpk, int* groups);
-int rows_max_workgroups(int nkv, int wpk, int groups, int cus);
-int launch_attention_rows(int nkv, int wpk, int groups, const AttnParams& p, hipStream_t stream);
+int rows_max_workgroups(int D, int nkv, int wpk, int groups, int cus);
+int launch_attention_rows(int D, int nkv, int wpk, int groups, const AttnParams& p, hipStream_t stream);
 int64_t attention_workspace_bytes(int B, int H, int KV, int D);
 int launch_attention(int mode, int D, AttnParams& p, void* workspace, int64_t ws_bytes,
                      hipStream_t stream);

@@ -111,21 +111,26 @@ def _run_batched(case: PagedCase, out_dtype=torch.float32, bt_dtype=torch.int32)
                                     # whole-row kernel: 4 KV heads x 1 wave, 2 KV heads x 2 waves,
                                     # several head groups per launch; odd KV falls back
                                     (16, 4, 128), (16, 2, 128), (24, 6, 128), (48, 6, 128), (64, 16, 128),
-                                    (12, 3, 128)])
+                                    (12, 3, 128),
+                                    # the same whole-row shapes at head_dim 64
+                                    (32, 4, 64), (32, 8, 64), (16, 4, 64), (16, 2, 64), (8, 2, 64),
+                                    (24, 6, 64), (64, 16, 64), (48, 6, 64)])
 def test_paged_batched_matches_oracle(H, KV, D):
     case = make_paged_case(seed=H * 131 + D, B=5, H=H, KV=KV, D=D, len_range=(1, 700))
     assert_close(_run_batched(case), paged_reference(case), what=f"H={H} KV={KV} D={D}")
 
 
 @pytest.mark.parametrize("bs", [1, 8, 16, 32, 48])
-def test_paged_block_sizes(bs):
-    case = make_paged_case(seed=bs, B=4, H=8, KV=2, D=128, block_size=bs, len_range=(1, 300))
-    assert_close(_run_batched(case), paged_reference(case), what=f"bs={bs}")
+@pytest.mark.parametrize("D", [64, 128])
+def test_paged_block_sizes(bs, D):
+    case = make_paged_case(seed=bs, B=4, H=8, KV=2, D=D, block_size=bs, len_range=(1, 300))
+    assert_close(_run_batched(case), paged_reference(case), what=f"bs={bs} D={D}")
 
 
-def test_paged_edge_lengths_and_formats():
+@pytest.mark.parametrize("D", [64, 128])
+def test_paged_edge_lengths_and_formats(D):
     """Lengths 0, 1, 15, 16, 17 and a long one; int64 tables; fp16 output."""
-    case = make_paged_case(seed=11, B=7, H=32, KV=8, D=128, lens=[0, 1, 15, 16, 17, 3000, 0])
+    case = make_paged_case(seed=11, B=7, H=32, KV=8, D=D, lens=[0, 1, 15, 16, 17, 3000, 0])
     ref = paged_reference(case)
     assert_close(_run_batched(case), ref, what="int32/fp32")
     assert_close(_run_batched(case, bt_dtype=torch.int64), ref, what="int64 tables")
@@ -161,11 +166,12 @@ def test_repeated_calls_reuse_workspace():
     assert np.array_equal(a, b)
 
 
-def test_split_sequences_alternating_inputs():
+@pytest.mark.parametrize("D", [64, 128])
+def test_split_sequences_alternating_inputs(D):
     """Sequences split over many workgroups, alternating two different inputs
     through the same workspace: each call must merge its own partials."""
-    a = make_paged_case(seed=31, B=2, H=32, KV=8, D=128, len_range=(6000, 9000))
-    b = make_paged_case(seed=32, B=3, H=32, KV=8, D=128, len_range=(3000, 9000))
+    a = make_paged_case(seed=31, B=2, H=32, KV=8, D=D, len_range=(6000, 9000))
+    b = make_paged_case(seed=32, B=3, H=32, KV=8, D=D, len_range=(3000, 9000))
     ra, rb = paged_reference(a), paged_reference(b)
     for i in range(3):
         assert_close(_run_batched(a), ra, what=f"a[{i}]")
