@@ -16,11 +16,22 @@ slower).  Before its W warmup steps, the benchmark therefore runs the decode
 untimed for --prewarm-ms (default 100 ms); the JSON line reports it.
 
 Printed: one JSON line with the throughput in algorithmic GB/s (packed KV +
-rulers, q, fp32 out, block-table entries and lengths actually read), the time
-per step, the roofline object for the decode kernel and a CPU baseline (the
-reference's CPU torch path on a bounded sample of the same workload).
+rulers, q, fp32 out, block-table entries and lengths actually read) over K
+back-to-back steps, the time per step, the roofline object for the decode
+kernel (its duration from an event pair around each of K further launches) and
+a CPU baseline (the reference's CPU torch path on a bounded sample of the same
+workload).
 
     python bench.py [--gpus 1] [--steps 500] [--warmup 400] [--prewarm-ms 100] [--no-cpu]
+                    [--workload headline|long-context|full-model-attention]
+
+--workload picks another decode shape for the same measurement (the default
+is the headline configuration above):
+* long-context: batch 8, lengths U[32768, 131072], 64 query / 8 KV heads,
+  head_dim 128, K/V ~ Student-t(3); also times the quantize-on-write append of
+  one new token per sequence;
+* full-model-attention: the attention of one layer of the full-model decode
+  step below, batch 32, lengths U[4096, 4224], 32 query / 4 KV heads, head_dim 64.
 
 --full-model instead prints the line of the full-model workload: greedy
 decode of a random-init Llama-style 1.1B model (22 layers, hidden 2048, 32 /
@@ -38,6 +49,7 @@ import platform
 import statistics
 import sys
 import time
+from dataclasses import dataclass
 from pathlib import Path
 
 ROOT = Path(__file__).resolve().parent
@@ -47,9 +59,52 @@ for _p in (ROOT / "slm-turbo_amd", ROOT):
 
 METRIC = "decode-attn µs/step + HBM GB/s (% of 8 TB/s), D=128 GQA paged 4-bit"
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E peak
-B, H, KV, D, BS = 64, 32, 8, 128, 16
-LEN_LO, LEN_HI = 512, 8192
-TRAFFIC_FILE = ROOT / "profiles" / "paged_decode_b64_h32_kv8_d128_traffic.txt"
+BS = 16
+
+
+@dataclass(frozen=True)
+class Workload:
+    """One decode step's shape: B sequences with lengths U[lo, hi] (seed 0),
+    H query / KV heads of head_dim D, K/V drawn from ``dist``; ``sets``
+    independent caches and queries are rotated per step."""
+    name: str
+    B: int
+    H: int
+    KV: int
+    D: int
+    lo: int
+    hi: int
+    dist: str
+    sets: int
+    text: str
+
+    @property
+    def tag(self) -> str:
+        return f"paged_decode_b{self.B}_h{self.H}_kv{self.KV}_d{self.D}"
+
+    @property
+    def metric(self) -> str:
+        if self.name == "headline":
+            return METRIC
+        return f"decode-attn µs/step + HBM GB/s (% of 8 TB/s), D={self.D} GQA paged 4-bit, {self.name}"
+
+
+WORKLOADS = {
+    "headline": Workload("headline", 64, 32, 8, 128, 512, 8192, "normal", 3,
+                         "paged per-token 4-bit decode attention, batch 64, lengths U[512,8192] seed 0, "
+                         "32 q / 8 KV heads, head_dim 128, block 16"),
+    "long-context": Workload("long-context", 8, 64, 8, 128, 32768, 131072, "t3", 2,
+                             "paged per-token 4-bit decode attention, batch 8, lengths U[32768,131072] seed 0, "
+                             "64 q / 8 KV heads, head_dim 128, block 16, K/V Student-t(3)"),
+    "full-model-attention": Workload("full-model-attention", 32, 32, 4, 64, 4096, 4224, "normal", 3,
+                                     "paged per-token 4-bit decode attention of one layer of the 1.1B "
+                                     "Llama-style decode step, batch 32, lengths U[4096,4224] seed 0, "
+                                     "32 q / 4 KV heads, head_dim 64, block 16"),
+}
+
+
+def traffic_file(w: Workload) -> Path:
+    return ROOT / "profiles" / f"{w.tag}_traffic.txt"
 
 
 def parse_args(argv=None):
@@ -60,7 +115,9 @@ def parse_args(argv=None):
     ap.add_argument("--prewarm-ms", type=float, default=100.0,
                     help="untimed decode launches for at least this long before the warmup steps")
     ap.add_argument("--seed", type=int, default=0)
-    ap.add_argument("--sets", type=int, default=3, help="independent cache/query sets rotated per step")
+    ap.add_argument("--workload", choices=sorted(WORKLOADS), default="headline")
+    ap.add_argument("--sets", type=int, default=0,
+                    help="independent cache/query sets rotated per step (0: the workload's own)")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="CPU baseline time budget")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--full-model", action="store_true",
@@ -73,13 +130,14 @@ def parse_args(argv=None):
     return ap.parse_args(argv)
 
 
-def build_workload(seed: int, sets: int, dev):
+def build_workload(seed: int, sets: int, dev, w: Workload = WORKLOADS["headline"]):
     import torch
 
     from kernels import kv_dequant as kd
 
+    B, H, KV, D = w.B, w.H, w.KV, w.D
     g = torch.Generator().manual_seed(seed)
-    lens = torch.randint(LEN_LO, LEN_HI + 1, (B,), generator=g)
+    lens = torch.randint(w.lo, w.hi + 1, (B,), generator=g)
     nblk = (lens + BS - 1) // BS
     total = int(nblk.sum())
     perm = torch.randperm(total, generator=g)
@@ -102,38 +160,50 @@ def build_workload(seed: int, sets: int, dev):
         qs.append(torch.randn((B, H, D), generator=g).half().to(dev))
         cache = torch.empty((total, BS, KV, D + 8), dtype=torch.uint8, device=dev)
         gg = torch.Generator(device=dev).manual_seed(seed * 1000 + s)
+
+        def values(n):
+            z = torch.randn((n, KV, D), generator=gg, device=dev)
+            if w.dist == "t3":                     # Student-t(3): z / sqrt(chi2_3 / 3)
+                chi2 = (torch.randn((3, n, KV, D), generator=gg, device=dev) ** 2).sum(0)
+                z = z / torch.sqrt(chi2 / 3.0)
+            return z.half()
+
         chunk = 1 << 16
         for t0 in range(0, N, chunk):
             n = min(chunk, N - t0)
-            k = torch.randn((n, KV, D), generator=gg, device=dev).half()
-            v = torch.randn((n, KV, D), generator=gg, device=dev).half()
+            k = values(n)
+            v = values(n)
             kd.kv_quantize_store(k, v, cache, slots[t0:t0 + n], BS)
         caches.append(cache)
     torch.cuda.synchronize()
     return lens, tables, qs, caches
 
 
-def algorithmic_bytes(lens) -> int:
+def algorithmic_bytes(lens, w: Workload = WORKLOADS["headline"]) -> int:
     """Bytes a perfect kernel must move per step: packed KV + rulers of every
     token, q (fp16), out (fp32), the block-table entries used and the lengths."""
+    B, H, KV, D = w.B, w.H, w.KV, w.D
     L = [int(x) for x in lens]
     blocks = sum((x + BS - 1) // BS for x in L)
     return sum(L) * KV * (D + 8) + B * H * D * 2 + B * H * D * 4 + blocks * 4 + B * 4
 
 
-def read_traffic():
+def read_traffic(w: Workload = WORKLOADS["headline"]):
     """HBM bytes per launch measured with rocprofv3 counters (committed summary)."""
-    if not TRAFFIC_FILE.exists():
+    path = traffic_file(w)
+    if not path.exists():
         return None
-    for line in TRAFFIC_FILE.read_text().splitlines():
+    for line in path.read_text().splitlines():
         if line.startswith("traffic_bytes_per_launch:"):
             return int(float(line.split(":", 1)[1]))
     return None
 
 
-def cpu_baseline(lens, tables, q, cache_gpu, out_gpu, budget_s: float):
+def cpu_baseline(lens, tables, q, cache_gpu, out_gpu, budget_s: float, w: Workload = WORKLOADS["headline"]):
     """The reference's CPU torch path (oracle/cpu_path.py) on a bounded sample."""
     import torch
+
+    B, H, KV, D = w.B, w.H, w.KV, w.D
 
     from oracle import cpu_path
 
@@ -231,9 +301,12 @@ def main(argv=None) -> int:
     from kernels import kv_dequant as kd
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
+    w = WORKLOADS[args.workload]
+    B, H, KV, D = w.B, w.H, w.KV, w.D
+    sets = args.sets or w.sets
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
-    lens, tables, qs, caches = build_workload(args.seed, args.sets, dev)
+    lens, tables, qs, caches = build_workload(args.seed, sets, dev, w)
     tables_d = tables.to(dev)
     lens_d = lens.to(torch.int32).to(dev)
     nb = caches[0].shape[0]
@@ -263,34 +336,41 @@ def main(argv=None) -> int:
     t_pre = time.perf_counter()
     while (time.perf_counter() - t_pre) * 1e3 < args.prewarm_ms:
         for i in range(16):
-            _native.check(lib, fn(*argsets[i % args.sets]))
+            _native.check(lib, fn(*argsets[i % sets]))
         torch.cuda.synchronize()
         prewarm += 16
     for i in range(args.warmup):
-        _native.check(lib, fn(*argsets[i % args.sets]))
+        _native.check(lib, fn(*argsets[i % sets]))
     torch.cuda.synchronize()
 
+    # Timed region: K steps back to back, events only at its ends (the whole-job
+    # rate).  Then K more steps with an event pair around every launch, for the
+    # kernel's own duration (the events between launches add a few µs of idle
+    # stream time per step, so they stay out of the first measurement).
     K = args.steps
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(K)]
     t_start, t_end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()                     # single process: the barrier is this sync
     t_start.record(stream)
     for i in range(K):
-        ev[i][0].record(stream)
-        fn(*argsets[i % args.sets])
-        ev[i][1].record(stream)
+        fn(*argsets[i % sets])
     t_end.record(stream)
     torch.cuda.synchronize()
     total_ms = t_start.elapsed_time(t_end)
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(K)]
+    for i in range(K):
+        ev[i][0].record(stream)
+        fn(*argsets[i % sets])
+        ev[i][1].record(stream)
+    torch.cuda.synchronize()
     launch_us = sorted(a.elapsed_time(b) * 1e3 for a, b in ev)
 
-    nbytes = algorithmic_bytes(lens)
+    nbytes = algorithmic_bytes(lens, w)
     ms_per_step = total_ms / K
     value = nbytes / (ms_per_step * 1e-3) / 1e9
     mean_launch = statistics.fmean(launch_us)
     achieved = nbytes / (mean_launch * 1e-6) / 1e9
     result = {
-        "metric": METRIC,
+        "metric": w.metric,
         "value": round(value, 2),
         "unit": "GB/s",
         "n_gpus": 1,
@@ -304,13 +384,13 @@ def main(argv=None) -> int:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "int4 codes; int32 (QK) / fp32 (PV) accumulate",
-        "data": "synthetic: K,V ~ N(0,1) fp16 quantized into the packed cache; q ~ N(0,1)",
+        "data": "synthetic: K,V ~ " + ("Student-t(3)" if w.dist == "t3" else "N(0,1)")
+                + " fp16 quantized into the packed cache; q ~ N(0,1)",
         "config": {
-            "workload": "paged per-token 4-bit decode attention, batch 64, lengths U[512,8192] seed 0, "
-                        "32 q / 8 KV heads, head_dim 128, block 16",
+            "workload": w.text,
             "batch": B, "num_heads": H, "num_kv_heads": KV, "head_dim": D, "block_size": BS,
             "total_tokens": int(lens.sum()), "algorithmic_bytes": nbytes,
-            "rotated_sets": args.sets, "out_dtype": "fp32",
+            "rotated_sets": sets, "out_dtype": "fp32",
         },
         "roofline": {
             "bound": "hbm",
@@ -318,7 +398,7 @@ def main(argv=None) -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": read_traffic(),
+            "traffic": read_traffic(w),
         },
         "launch_us": {
             "mean": round(mean_launch, 2),
@@ -328,11 +408,38 @@ def main(argv=None) -> int:
         },
     }
     if not args.no_cpu:
-        result["cpu_baseline"] = cpu_baseline(lens, tables, qs[0], caches[0], ref_out, args.cpu_seconds)
+        result["cpu_baseline"] = cpu_baseline(lens, tables, qs[0], caches[0], ref_out, args.cpu_seconds, w)
     else:
         result["cpu_baseline"] = None
+    result["append"] = time_append(kd, caches[-1], tables, lens, w, dev)
     print(json.dumps(result))
     return 0
+
+
+def time_append(kd, cache, tables, lens, w: Workload, dev, calls: int = 200) -> dict:
+    """Quantize-on-write of one new token per sequence (the decode step's
+    append), timed over ``calls`` back-to-back launches.  It rewrites each
+    sequence's last slot, so it runs after everything that reads the cache."""
+    import torch
+
+    g = torch.Generator(device=dev).manual_seed(7)
+    k = torch.randn((w.B, w.KV, w.D), generator=g, device=dev).half()
+    v = torch.randn((w.B, w.KV, w.D), generator=g, device=dev).half()
+    last = (lens - 1).long()
+    slots = (tables[torch.arange(w.B), last // BS].long() * BS + last % BS).to(dev)
+    for _ in range(20):
+        kd.kv_quantize_store(k, v, cache, slots, BS)
+    stream = torch.cuda.current_stream(dev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for _ in range(calls):
+        kd.kv_quantize_store(k, v, cache, slots, BS)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / calls
+    return {"tokens": w.B, "us_per_call": round(us, 2),
+            "note": "one new token per sequence, K/V fp16 in, packed slot + rulers out; launch-latency bound"}
 
 
 if __name__ == "__main__":

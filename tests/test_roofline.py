@@ -87,6 +87,21 @@ def test_decode_bytes_match_the_benchmark_formula():
     assert rl.decode_attention_bytes(lens.tolist(), 32, 8, 128, 16) == bench.algorithmic_bytes(lens)
 
 
+@pytest.mark.parametrize("name", ["headline", "long-context", "full-model-attention"])
+def test_benchmark_workloads_have_traffic_summaries(name):
+    """Every bench.py workload has a committed counter summary whose HBM bytes
+    per launch sit just above the algorithmic bytes of its seeded lengths."""
+    import bench
+
+    w = bench.WORKLOADS[name]
+    g = torch.Generator().manual_seed(0)
+    lens = torch.randint(w.lo, w.hi + 1, (w.B,), generator=g)
+    alg = bench.algorithmic_bytes(lens, w)
+    assert alg == rl.decode_attention_bytes(lens.tolist(), w.H, w.KV, w.D, bench.BS)
+    traffic = bench.read_traffic(w)
+    assert traffic is not None and 1.0 <= traffic / alg < 1.1
+
+
 def test_decode_attention_intensity_is_below_the_ridge():
     """4-bit paged decode at G = 4 is memory bound on MI355X by the flop roof
     (~15 flop/B against a ~19.7 flop/B ridge)."""
