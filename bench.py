@@ -33,6 +33,11 @@ is the headline configuration above):
 * full-model-attention: the attention of one layer of the full-model decode
   step below, batch 32, lengths U[4096, 4224], 32 query / 4 KV heads, head_dim 64.
 
+--op-level prints the reference's op-level tables (one JSON line per case):
+per-channel decode (32/4 and 14/2 heads at head_dim 64, 32/8 at 128; S = 512,
+1024, 2048) and causal prefill (32/4 and 14/2 at 64; S = 512, 1024), each
+against fp16 SDPA over the dequantized K/V broadcast to the query heads.
+
 --full-model instead prints the line of the full-model workload: greedy
 decode of a random-init Llama-style 1.1B model (22 layers, hidden 2048, 32 /
 4 heads, head_dim 64, MLP 5632), batch 32, prompt 4096 random token ids, 128
@@ -120,6 +125,8 @@ def parse_args(argv=None):
                     help="independent cache/query sets rotated per step (0: the workload's own)")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="CPU baseline time budget")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--op-level", action="store_true",
+                    help="the reference's op-level per-channel decode/prefill tables instead of the paged decode")
     ap.add_argument("--full-model", action="store_true",
                     help="time full-model greedy decode (1.1B Llama-style) instead of the kernel")
     ap.add_argument("--fm-batch", type=int, default=32)
@@ -244,6 +251,76 @@ def cpu_baseline(lens, tables, q, cache_gpu, out_gpu, budget_s: float, w: Worklo
     }
 
 
+def op_level(args) -> int:
+    """The reference's op-level tables (kernels/benchmark/benchmark.py:106-174) on this
+    GPU: per-channel decode and causal prefill through the HIP kernels against fp16 SDPA
+    over the dequantized K/V broadcast to the query heads.  One JSON line per case."""
+    import torch
+    import torch.nn.functional as F
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+
+    from kernels import kv_dequant as kd
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+
+    def timeit(fn, iters, warmup=5):
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        for _ in range(iters):
+            fn()
+        e.record()
+        torch.cuda.synchronize()
+        return s.elapsed_time(e) / iters * 1e3           # µs per call
+
+    def dequant(packed, scale, zero):                    # (codes - zero) * scale, fp32
+        codes = torch.stack([packed & 15, packed >> 4], dim=-1).flatten(-2).float()
+        return (codes - zero.float()[:, None, :]) * scale.float()[:, None, :]
+
+    def sdpa(q, k, v, causal):
+        with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+            return F.scaled_dot_product_attention(q[None], k[None], v[None], is_causal=causal)[0]
+
+    cases = [("decode", H, KV, D, S, 200) for H, KV, D in ((32, 4, 64), (14, 2, 64), (32, 8, 128))
+             for S in (512, 1024, 2048)]
+    cases += [("prefill", H, KV, D, S, 50) for H, KV, D in ((32, 4, 64), (14, 2, 64)) for S in (512, 1024)]
+    for phase, H, KV, D, S, iters in cases:
+        g = torch.Generator(device=dev).manual_seed(0)
+        M = 1 if phase == "decode" else S
+        q = torch.randn((H, M, D), generator=g, device=dev).half()
+        k = torch.randn((KV, S, D), generator=g, device=dev).half()
+        v = torch.randn((KV, S, D), generator=g, device=dev).half()
+        kp, ks, kz, vp, vs, vz = kd.quantize_kv(k, v)
+        kb = dequant(kp, ks, kz).half().repeat_interleave(H // KV, dim=0)
+        vb = dequant(vp, vs, vz).half().repeat_interleave(H // KV, dim=0)
+        causal = phase == "prefill"
+        if causal:
+            run = lambda: kd.kv_dequant_prefill_attention(q, kp, ks, kz, vp, vs, vz, causal=True, num_kv_heads=KV)
+        else:
+            run = lambda: kd.kv_dequant_decode_attention(q, kp, ks, kz, vp, vs, vz, num_kv_heads=KV)
+        out = run()
+        line = {"metric": f"op-level {phase} µs/call, per-channel 4-bit vs fp16 SDPA", "phase": phase,
+                "H": H, "KV": KV, "D": D, "S": S, "kernel_us": round(timeit(run, iters), 2)}
+        try:
+            ref = sdpa(q, kb, vb, causal)
+            line["err_vs_dequantized"] = float((out - ref.float()).abs().max())
+            line["fp16_sdpa_us"] = round(timeit(lambda: sdpa(q, kb, vb, causal), iters), 2)
+            line["speedup_vs_fp16_sdpa"] = round(line["fp16_sdpa_us"] / line["kernel_us"], 3)
+        except RuntimeError as e:                         # no flash / memory-efficient kernel here
+            line["fp16_sdpa_us"] = None
+            line["fp16_sdpa_error"] = str(e).splitlines()[0][:160]
+        packed_bytes = 2 * KV * S * (D // 2) + 4 * KV * D * 2
+        line["kv_bytes"] = {"fp16_broadcast": 2 * H * S * D * 2, "packed": packed_bytes}
+        if phase == "decode":
+            line["packed_gb_per_s"] = round(packed_bytes / line["kernel_us"] / 1e3, 2)
+        print(json.dumps(line), flush=True)
+    return 0
+
+
 def full_model(args) -> int:
     """One JSON line: tokens/s of greedy decode, packed 4-bit KV vs fp16 eager."""
     import torch
@@ -294,6 +371,8 @@ def main(argv=None) -> int:
         return 2
     if args.full_model:
         return full_model(args)
+    if args.op_level:
+        return op_level(args)
 
     import torch
 

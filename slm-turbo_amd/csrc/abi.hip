@@ -299,6 +299,10 @@ int slmt_prefill_per_channel(const void* q, const void* k_packed, const void* k_
   if (rc != SLMT_OK) return rc;
   if (num_queries < 0) return fail(SLMT_ERR_INVALID, "kv_dequant_prefill: M must be >= 0");
   if (num_queries == 0) return SLMT_OK;
+  if (prefill_mfma_supported(head_dim))
+    return launch_prefill_mfma(q, k_packed, k_scale, k_zero, v_packed, v_scale, v_zero, num_heads,
+                               num_heads / num_kv_heads, num_queries, seq_len, head_dim, causal, use_quant, out,
+                               reinterpret_cast<hipStream_t>(stream));
   rc = check_workspace(ph, num_queries, num_heads, num_kv_heads, head_dim, workspace, workspace_bytes);
   if (rc != SLMT_OK) return rc;
   AttnParams p = blank_params();

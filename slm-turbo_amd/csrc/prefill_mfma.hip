@@ -1,0 +1,315 @@
+// Per-channel 4-bit prefill attention on the matrix cores (gfx950 MFMA), head_dim 64
+// and 128 (reference kernel it replaces: kv_dequant_prefill_kernel,
+// kernels/kv_dequant_kernels.cuh:293-502).
+//
+// Prefill is GEMM-shaped (every key meets up to 64 query rows of a tile), so
+// unlike the decode it runs on the matrix cores.  A workgroup takes 64 query rows
+// of one query head, one wave per 16 rows, and walks the 64-key tiles the rows
+// can see.  Everything is kept transposed, so a lane owns one query column from
+// the scores to the output:
+//   S^T = K Q'^T     (v_mfma_f32_16x16x32_f16: A = K rows, B = the lane's query)
+//   P^T = exp2(S^T - m)      (online softmax per query column)
+//   O^T += V^T P^T   (v_mfma_f32_16x16x16f16: B = the lane's P^T block as is)
+//
+// Exactness of the operands (a nibble becomes the fp16 1024 + code by one OR with
+// the pattern 0x6400; subtracting an integer below 2048 from it is exact):
+// * K enters as its codes n.  The reference's q.k = sum q_d s_d (n_d - z_d), and
+//   sum q_d s_d z_d is the same for every key of a query row, so it cancels in
+//   the softmax and is never formed.
+// * The per-channel K scale folds into the query: q'_d = q_d * s_d in fp32,
+//   split into an fp16 high part and the fp16 rounding of the remainder; two
+//   products per block keep ~22 bits of q'.
+// * V enters as n - zr, zr the zero point rounded and clamped to 0..15 (the
+//   reference quantizer's zero points are such integers), and the finished row
+//   is o_d = s_d * (sum p (n - zr) / l - (z_d - zr_d)) in fp32.
+// * P enters in fp16 (relative 2^-11 per weight), as the decode's weights do.
+// use_quant = 0 takes the raw codes (scale 1, zero 0).  Causal row m sees keys
+// n <= m; keys past S are masked.  S = 0 yields NaN rows (0/0), as the
+// reference's kernels do.
+//
+// Staging: the workgroup converts each tile into a 2-stage LDS ring: K as
+// [key][dim] fp16 rows padded to D*2+16 bytes (16-byte operand reads of 8 rows at
+// once hit 8 disjoint bank groups), V^T as [dim][key] fp16 rows padded to 136
+// bytes (8-byte reads of 16 rows hit 16 disjoint bank pairs).  The next tile's
+// codes are loaded into registers before the current tile's products and
+// written after them; one barrier per tile.
+#include "slmt_internal.h"
+
+namespace slmt {
+namespace prefill {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+struct Params {
+  const uint16_t* q;                       // [H, M, D] fp16
+  const uint8_t* kp;                       // [KV_t, S, D/2] codes
+  const uint8_t* vp;
+  const uint16_t *ks, *kz, *vs, *vz;       // [KV_t, D] fp16 scale / zero point
+  float* out;                              // [H, M, D]
+  int H, G, M, S, causal, use_quant, qblocks;
+};
+
+constexpr int BM = 64;   // query rows per workgroup
+constexpr int BN = 64;   // keys per tile
+
+template <int D>
+struct Geo {
+  static constexpr int KROW = D * 2 + 16;   // bytes of a staged K row
+  static constexpr int VROW = BN * 2 + 8;   // bytes of a staged V^T row
+  static constexpr int KBYTES = BN * KROW;
+  static constexpr int STAGE = KBYTES + D * VROW;
+  static constexpr int LDS = 2 * STAGE;
+  static constexpr int KW = D / 64;         // 8-byte K words per staging thread (K: 4 threads per key)
+  static constexpr int VW = D / 64;         // V dwords per key per staging thread (V: 8 threads per key pair)
+};
+
+__device__ __forceinline__ float hf(uint16_t h) { return h2f(h); }
+
+// fp16 pairs (1024 + low nibble, 1024 + high nibble) of byte i of x, minus zc
+__device__ __forceinline__ uint32_t nib_pair(uint32_t lo_all, uint32_t hi_all, int i, half2v zc) {
+  const uint32_t w = __builtin_amdgcn_perm(hi_all, lo_all, 0x0C000C00u | ((4u + i) << 16) | (uint32_t)i) | 0x64006400u;
+  const half2v r = __builtin_bit_cast(half2v, w) - zc;
+  return __builtin_bit_cast(uint32_t, r);
+}
+
+template <int D>
+__global__ void __launch_bounds__(256) prefill_kernel(const Params p) {
+  using GG = Geo<D>;
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int h = blockIdx.x % p.H;
+  const int qb = p.qblocks - 1 - (int)(blockIdx.x / p.H);   // the longest query blocks first
+  const int kv = h / p.G;
+  const int m0 = qb * BM;
+  const int col = lane & 15, grp = lane >> 4;
+  const int m = m0 + 16 * w + col;                          // this lane's query row
+  const int mq = min(m, p.M - 1);
+  const int kend = p.causal ? min(p.S, m0 + BM) : p.S;
+  const int ntiles = (kend + BN - 1) / BN;
+  const bool quant = p.use_quant != 0;
+
+  // ---- the lane's query column, scaled per channel and split hi / lo (B operand of S^T)
+  half8 qh[D / 32], ql[D / 32];
+  {
+    const uint16_t* qrow = p.q + ((int64_t)h * p.M + mq) * D;
+#pragma unroll
+    for (int j = 0; j < D / 32; ++j) {
+      const uint4 raw = *reinterpret_cast<const uint4*>(qrow + 32 * j + 8 * grp);
+      const uint32_t wds[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int d = 32 * j + 8 * grp + e;
+        float x = hf((uint16_t)(wds[e >> 1] >> (16 * (e & 1))));
+        if (quant) x *= hf(p.ks[(int64_t)kv * D + d]);
+        const _Float16 hi = (_Float16)x;
+        qh[j][e] = hi;
+        ql[j][e] = (_Float16)(x - (float)hi);
+      }
+    }
+  }
+
+  // ---- staging roles
+  // K: thread (key kk = tid / 4, quarter ku = tid % 4): dims D/4 * ku .. + D/4 - 1
+  const int kk = tid >> 2, ku = tid & 3;
+  const half2v kzc = half2v{(_Float16)1024.0f, (_Float16)1024.0f};
+  // V: thread (key pair vk = tid / 8, byte group vb = tid % 8 (+ 8)): dims 8 vb .. 8 vb + 7,
+  // each with 1024 + its rounded zero point
+  const int vk = tid >> 3, vb = tid & 7;
+  auto zround = [&](int d) { return quant ? fminf(fmaxf(__builtin_rintf(hf(p.vz[(int64_t)kv * D + d])), 0.f), 15.f) : 0.f; };
+  half2v vzc[GG::VW][8];
+#pragma unroll
+  for (int r = 0; r < GG::VW; ++r)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const _Float16 z = (_Float16)(1024.0f + zround(8 * (vb + 8 * r) + i));
+      vzc[r][i][0] = z;
+      vzc[r][i][1] = z;
+    }
+  const uint8_t* kbase = p.kp + (int64_t)kv * p.S * (D / 2);
+  const uint8_t* vbase = p.vp + (int64_t)kv * p.S * (D / 2);
+  uint2 kx[GG::KW];
+  uint32_t vx[GG::VW][2];
+  auto load = [&](int t) {   // the tile's codes into registers (keys past S re-read key S - 1)
+    const int key = min(t * BN + kk, p.S - 1);
+    const uint8_t* ksrc = kbase + (int64_t)key * (D / 2) + ku * (D / 8);
+#pragma unroll
+    for (int i = 0; i < GG::KW; ++i) kx[i] = *reinterpret_cast<const uint2*>(ksrc + 8 * i);
+    const int k0 = min(t * BN + 2 * vk, p.S - 1), k1 = min(t * BN + 2 * vk + 1, p.S - 1);
+#pragma unroll
+    for (int r = 0; r < GG::VW; ++r) {
+      vx[r][0] = *reinterpret_cast<const uint32_t*>(vbase + (int64_t)k0 * (D / 2) + 4 * (vb + 8 * r));
+      vx[r][1] = *reinterpret_cast<const uint32_t*>(vbase + (int64_t)k1 * (D / 2) + 4 * (vb + 8 * r));
+    }
+  };
+  auto store = [&](int buf) {  // registers -> fp16 (code - zero) in LDS stage buf
+    uint8_t* Ks = smem + buf * GG::STAGE;
+    uint8_t* Vs = Ks + GG::KBYTES;
+    uint32_t kw[D / 8];
+#pragma unroll
+    for (int i = 0; i < GG::KW; ++i) {
+      const uint32_t ws2[2] = {kx[i].x, kx[i].y};
+#pragma unroll
+      for (int hw = 0; hw < 2; ++hw) {
+        const uint32_t lo = ws2[hw] & 0x0F0F0F0Fu, hi = (ws2[hw] >> 4) & 0x0F0F0F0Fu;
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+          const int pi = 8 * i + 4 * hw + b;     // dim pair index within the thread's quarter
+          kw[pi] = nib_pair(lo, hi, b, kzc);
+        }
+      }
+    }
+    uint4* kd = reinterpret_cast<uint4*>(Ks + kk * GG::KROW + ku * (D / 2));
+#pragma unroll
+    for (int i = 0; i < D / 32; ++i) kd[i] = make_uint4(kw[4 * i], kw[4 * i + 1], kw[4 * i + 2], kw[4 * i + 3]);
+#pragma unroll
+    for (int r = 0; r < GG::VW; ++r) {
+      const uint32_t lo0 = vx[r][0] & 0x0F0F0F0Fu, hi0 = (vx[r][0] >> 4) & 0x0F0F0F0Fu;
+      const uint32_t lo1 = vx[r][1] & 0x0F0F0F0Fu, hi1 = (vx[r][1] >> 4) & 0x0F0F0F0Fu;
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        const int d = 8 * (vb + 8 * r) + 2 * b;  // dims d (low nibbles) and d + 1 (high nibbles)
+        const uint32_t sel = 0x0C000C00u | ((4u + b) << 16) | (uint32_t)b;
+        const half2v e = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(lo1, lo0, sel) | 0x64006400u) - vzc[r][2 * b];
+        const half2v o = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(hi1, hi0, sel) | 0x64006400u) - vzc[r][2 * b + 1];
+        *reinterpret_cast<uint32_t*>(Vs + d * GG::VROW + 4 * vk) = __builtin_bit_cast(uint32_t, e);
+        *reinterpret_cast<uint32_t*>(Vs + (d + 1) * GG::VROW + 4 * vk) = __builtin_bit_cast(uint32_t, o);
+      }
+    }
+  };
+
+  floatx4 o[D / 16];
+#pragma unroll
+  for (int c = 0; c < D / 16; ++c) o[c] = floatx4{0.f, 0.f, 0.f, 0.f};
+  float m_run = -INFINITY, l_run = 0.f;
+  const float sc = 1.4426950408889634f * __builtin_amdgcn_rsqf((float)D);
+
+  if (ntiles > 0) {
+    load(0);
+    store(0);
+  }
+  __syncthreads();
+  for (int t = 0; t < ntiles; ++t) {
+    const int buf = t & 1;
+    if (t + 1 < ntiles) load(t + 1);
+    const uint8_t* Ks = smem + buf * GG::STAGE;
+    const uint8_t* Vs = Ks + GG::KBYTES;
+    // S^T: keys 16 n + 4 grp + i of this tile against the lane's query
+    floatx4 s[4];
+#pragma unroll
+    for (int n = 0; n < 4; ++n) {
+      s[n] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int j = 0; j < D / 32; ++j) {
+        const half8 a = *reinterpret_cast<const half8*>(Ks + (16 * n + col) * GG::KROW + (32 * j + 8 * grp) * 2);
+        s[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qh[j], s[n], 0, 0, 0);
+        s[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, ql[j], s[n], 0, 0, 0);
+      }
+    }
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int n = 0; n < 4; ++n)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int key = t * BN + 16 * n + 4 * grp + i;
+        const bool ok = key < p.S && (!p.causal || key <= m);
+        const float v = ok ? s[n][i] * sc : -INFINITY;
+        s[n][i] = v;
+        tmax = fmaxf(tmax, v);
+      }
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+    const float m_new = fmaxf(m_run, tmax);                  // finite: key 0 is visible to every row
+    const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+    half4 pb[4];
+    float ls = 0.f;
+#pragma unroll
+    for (int n = 0; n < 4; ++n)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float pv = __builtin_amdgcn_exp2f(s[n][i] - m_new);
+        ls += pv;
+        pb[n][i] = (_Float16)pv;
+      }
+    l_run = l_run * alpha + ls;
+    m_run = m_new;
+#pragma unroll
+    for (int c = 0; c < D / 16; ++c) o[c] *= alpha;
+    // O^T: dims 16 c + 4 grp + i
+#pragma unroll
+    for (int c = 0; c < D / 16; ++c)
+#pragma unroll
+      for (int n = 0; n < 4; ++n) {
+        const half4 a = *reinterpret_cast<const half4*>(Vs + (16 * c + col) * GG::VROW + (16 * n + 4 * grp) * 2);
+        o[c] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, pb[n], o[c], 0, 0, 0);
+      }
+    if (t + 1 < ntiles) store(buf ^ 1);
+    __syncthreads();
+  }
+
+  // the 4 lane groups of a column hold disjoint keys: add their sums
+  float lt = l_run + __shfl_xor(l_run, 16, 64);
+  lt += __shfl_xor(lt, 32, 64);
+  const float rl = 1.0f / lt;
+  if (m < p.M) {
+    float* orow = p.out + ((int64_t)h * p.M + m) * D;
+#pragma unroll
+    for (int c = 0; c < D / 16; ++c) {
+      float v[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int d = 16 * c + 4 * grp + i;
+        v[i] = o[c][i] * rl;
+        if (quant) v[i] = (v[i] - (hf(p.vz[(int64_t)kv * D + d]) - zround(d))) * hf(p.vs[(int64_t)kv * D + d]);
+      }
+      *reinterpret_cast<float2*>(orow + 16 * c + 4 * grp) = make_float2(v[0], v[1]);
+      *reinterpret_cast<float2*>(orow + 16 * c + 4 * grp + 2) = make_float2(v[2], v[3]);
+    }
+  }
+}
+
+template <int D>
+int launch(const Params& p, hipStream_t stream) {
+  static const bool lds_ok = [] {   // above 64 KB of LDS (head_dim 128) needs the attribute
+    return hipFuncSetAttribute(reinterpret_cast<const void*>(prefill_kernel<D>),
+                               hipFuncAttributeMaxDynamicSharedMemorySize, Geo<D>::LDS) == hipSuccess;
+  }();
+  if (!lds_ok) return fail(SLMT_ERR_HIP, "prefill: could not grant the kernel its LDS");
+  const int grid = p.qblocks * p.H;
+  hipLaunchKernelGGL(prefill_kernel<D>, dim3(grid), dim3(256), Geo<D>::LDS, stream, p);
+  return check_launch("prefill");
+}
+
+}  // namespace prefill
+
+bool prefill_mfma_supported(int D) { return D == 64 || D == 128; }
+
+int launch_prefill_mfma(const void* q, const void* kp, const void* ks, const void* kz, const void* vp, const void* vs,
+                        const void* vz, int H, int G, int M, int S, int D, int causal, int use_quant, float* out,
+                        hipStream_t stream) {
+  prefill::Params p;
+  p.q = reinterpret_cast<const uint16_t*>(q);
+  p.kp = reinterpret_cast<const uint8_t*>(kp);
+  p.vp = reinterpret_cast<const uint8_t*>(vp);
+  p.ks = reinterpret_cast<const uint16_t*>(ks);
+  p.kz = reinterpret_cast<const uint16_t*>(kz);
+  p.vs = reinterpret_cast<const uint16_t*>(vs);
+  p.vz = reinterpret_cast<const uint16_t*>(vz);
+  p.out = out;
+  p.H = H;
+  p.G = G;
+  p.M = M;
+  p.S = S;
+  p.causal = causal ? 1 : 0;
+  p.use_quant = use_quant ? 1 : 0;
+  p.qblocks = (M + prefill::BM - 1) / prefill::BM;
+  if (M <= 0) return SLMT_OK;
+  if ((int64_t)p.qblocks * H > 0x7fffffff) return fail(SLMT_ERR_UNSUPPORTED, "prefill: too many query blocks");
+  if (D == 64) return prefill::launch<64>(p, stream);
+  if (D == 128) return prefill::launch<128>(p, stream);
+  return fail(SLMT_ERR_UNSUPPORTED, "prefill: the matrix-core kernel takes head_dim 64 or 128");
+}
+
+}  // namespace slmt

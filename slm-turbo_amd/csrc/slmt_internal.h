@@ -218,6 +218,13 @@ bool rows_shape(int H, int G, int D, int cache_kv, int* nkv, int* wpk, int* grou
 int rows_max_workgroups(int D, int nkv, int wpk, int groups, int cus);
 int launch_attention_rows(int D, int nkv, int wpk, int groups, const AttnParams& p, hipStream_t stream);
 int64_t attention_workspace_bytes(int B, int H, int KV, int D);
+
+// Per-channel prefill on the matrix cores (prefill_mfma.hip), head_dim 64 and 128;
+// no workspace.  q [H, M, D] fp16, codes [KV_t, S, D/2], rulers [KV_t, D].
+bool prefill_mfma_supported(int D);
+int launch_prefill_mfma(const void* q, const void* kp, const void* ks, const void* kz, const void* vp, const void* vs,
+                        const void* vz, int H, int G, int M, int S, int D, int causal, int use_quant, float* out,
+                        hipStream_t stream);
 int launch_attention(int mode, int D, AttnParams& p, void* workspace, int64_t ws_bytes,
                      hipStream_t stream);
 

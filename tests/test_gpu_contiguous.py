@@ -135,6 +135,66 @@ def test_prefill_per_channel(H, KV, D, M, S, causal):
     assert_close(out.cpu().numpy(), ref, what="prefill")
 
 
+def _pf_inputs(seed, H, KV, M, S, D, outliers=False, t3=False):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(H, M, D, generator=g).half()
+    if t3:
+        k, v = kv_values(g, (KV, S, D), "t3"), kv_values(g, (KV, S, D), "t3")
+    else:
+        k, v = torch.randn(KV, S, D, generator=g), torch.randn(KV, S, D, generator=g)
+    if outliers:
+        k, v = _outliers(k, g), _outliers(v, g)
+    kp, ks, kz, vp, vs, vz = oq.quantize_kv(k.half().numpy(), v.half().numpy())
+    return q, [torch.from_numpy(a) for a in (kp, ks, kz, vp, vs, vz)]
+
+
+def _prefill(q, t, **kw):
+    out = _kd().kv_dequant_prefill_attention(q.to(DEV), *[x.to(DEV) for x in t], **kw)
+    torch.cuda.synchronize()
+    return out.cpu().numpy()
+
+
+# head_dim 64 and 128 run on the matrix-core kernel: query blocks of 64 rows,
+# key tiles of 64, so these cover partial blocks and tiles, M > S and M < S
+@pytest.mark.parametrize("H,KV,D,M,S,causal,outl,t3", [
+    (32, 4, 64, 512, 512, True, False, False),     # the reference's op-level prefill shapes
+    (14, 2, 64, 1024, 1024, True, False, False),
+    (12, 2, 128, 300, 300, True, True, False),      # config-2 heads, 1 % outlier channels x8
+    (8, 2, 128, 129, 1000, False, False, True),     # Student-t K/V, non-causal
+    (8, 8, 64, 65, 63, True, True, False),          # M > S
+    (4, 1, 128, 1, 777, True, False, False),        # a single row
+    (16, 2, 64, 200, 1500, True, False, True)])     # M < S
+def test_prefill_matrix_cores(H, KV, D, M, S, causal, outl, t3):
+    q, t = _pf_inputs(H + M + S, H, KV, M, S, D, outl, t3)
+    out = _prefill(q, t, causal=causal, num_kv_heads=KV)
+    ref = oa.prefill_per_channel(q.numpy(), *[x.numpy() for x in t], causal=causal)
+    assert_close(out, ref, what=f"prefill H={H} KV={KV} D={D} M={M} S={S}")
+
+
+def test_prefill_matrix_cores_raw_nibbles_and_tensor_heads():
+    """use_quant=False (raw codes), and num_kv_heads < k_packed.shape[0]."""
+    q, t = _pf_inputs(9, 8, 4, 100, 300, 64)
+    out = _prefill(q, t, causal=True, use_quant=False, num_kv_heads=4)
+    ref = oa.prefill_per_channel(q.numpy(), *[x.numpy() for x in t], causal=True, use_quant=False)
+    assert_close(out, ref, what="use_quant=False")
+    out = _prefill(q, t, causal=True, num_kv_heads=2)
+    kp, ks, kz, vp, vs, vz = [x.numpy() for x in t]
+    ref = oa.prefill_per_channel(q.numpy(), kp[:2], ks[:2], kz[:2], vp[:2], vs[:2], vz[:2], causal=True)
+    assert_close(out, ref, what="num_kv_heads=2 of 4")
+
+
+def test_prefill_matrix_cores_fractional_zero_points():
+    """Zero points need not be integers: the kernel takes the integer part into
+    the operand and the rest in fp32."""
+    q, t = _pf_inputs(10, 8, 2, 130, 200, 128)
+    g = torch.Generator().manual_seed(3)
+    t[2] = (t[2].float() + torch.rand(t[2].shape, generator=g) * 3 - 1.5).half()   # k_zero
+    t[5] = (t[5].float() + torch.rand(t[5].shape, generator=g) * 3 - 1.5).half()   # v_zero
+    out = _prefill(q, t, causal=True, num_kv_heads=2)
+    ref = oa.prefill_per_channel(q.numpy(), *[x.numpy() for x in t], causal=True)
+    assert_close(out, ref, what="fractional zero points")
+
+
 # ------------------------------------------------------------------ per-token contiguous decode
 @pytest.mark.parametrize("H,KV,D,S", [(32, 8, 128, 1000), (4, 4, 64, 17), (12, 2, 80, 333)])
 def test_decode_per_token_contiguous(H, KV, D, S):
