@@ -288,7 +288,9 @@ def op_level(args) -> int:
     cases = [("decode", H, KV, D, S, 200) for H, KV, D in ((32, 4, 64), (14, 2, 64), (32, 8, 128))
              for S in (512, 1024, 2048)]
     cases += [("prefill", H, KV, D, S, 50) for H, KV, D in ((32, 4, 64), (14, 2, 64)) for S in (512, 1024)]
-    for phase, H, KV, D, S, iters in cases:
+    # beyond the reference's table: prefills long enough to be compute-bound
+    extra = [("prefill", 32, 4, 64, 4096, 10), ("prefill", 12, 2, 128, 4096, 10)]
+    for phase, H, KV, D, S, iters in cases + extra:
         g = torch.Generator(device=dev).manual_seed(0)
         M = 1 if phase == "decode" else S
         q = torch.randn((H, M, D), generator=g, device=dev).half()
@@ -317,6 +319,10 @@ def op_level(args) -> int:
         line["kv_bytes"] = {"fp16_broadcast": 2 * H * S * D * 2, "packed": packed_bytes}
         if phase == "decode":
             line["packed_gb_per_s"] = round(packed_bytes / line["kernel_us"] / 1e3, 2)
+        else:   # causal: QK and PV over the S (S + 1) / 2 visible pairs, 2 flops per multiply-add
+            line["tflops"] = round(4.0 * H * D * S * (S + 1) / 2 / line["kernel_us"] / 1e6, 2)
+        if (phase, H, KV, D, S, iters) in extra:
+            line["extra"] = "beyond the reference's op-level table"
         print(json.dumps(line), flush=True)
     return 0
 

@@ -31,9 +31,11 @@
 // [key][dim] fp16 rows padded to D*2+16 bytes (16-byte operand reads of 8 rows at
 // once hit 8 disjoint bank groups), V^T as [dim][key] fp16 rows padded to 136
 // bytes (8-byte reads of 16 rows hit 16 disjoint bank pairs).  The next tile's
-// codes are loaded into registers before the current tile's products and
-// written after them; one barrier per tile.
+// codes are loaded into registers two tiles ahead and written to LDS after the
+// current tile's products; one barrier per tile.
 #include "slmt_internal.h"
+
+#include <type_traits>
 
 namespace slmt {
 namespace prefill {
@@ -130,27 +132,31 @@ __global__ void __launch_bounds__(256) prefill_kernel(const Params p) {
     }
   const uint8_t* kbase = p.kp + (int64_t)kv * p.S * (D / 2);
   const uint8_t* vbase = p.vp + (int64_t)kv * p.S * (D / 2);
-  uint2 kx[GG::KW];
-  uint32_t vx[GG::VW][2];
-  auto load = [&](int t) {   // the tile's codes into registers (keys past S re-read key S - 1)
+  // Two register slots of codes: tile k is loaded into slot k % 2 two tiles
+  // before it is computed, and written to LDS one tile before.
+  uint2 kx[2][GG::KW];
+  uint32_t vx[2][GG::VW][2];
+  auto load = [&](int t, auto slot) {   // the tile's codes (keys past S re-read key S - 1)
+    constexpr int sl = decltype(slot)::value;
     const int key = min(t * BN + kk, p.S - 1);
     const uint8_t* ksrc = kbase + (int64_t)key * (D / 2) + ku * (D / 8);
 #pragma unroll
-    for (int i = 0; i < GG::KW; ++i) kx[i] = *reinterpret_cast<const uint2*>(ksrc + 8 * i);
+    for (int i = 0; i < GG::KW; ++i) kx[sl][i] = *reinterpret_cast<const uint2*>(ksrc + 8 * i);
     const int k0 = min(t * BN + 2 * vk, p.S - 1), k1 = min(t * BN + 2 * vk + 1, p.S - 1);
 #pragma unroll
     for (int r = 0; r < GG::VW; ++r) {
-      vx[r][0] = *reinterpret_cast<const uint32_t*>(vbase + (int64_t)k0 * (D / 2) + 4 * (vb + 8 * r));
-      vx[r][1] = *reinterpret_cast<const uint32_t*>(vbase + (int64_t)k1 * (D / 2) + 4 * (vb + 8 * r));
+      vx[sl][r][0] = *reinterpret_cast<const uint32_t*>(vbase + (int64_t)k0 * (D / 2) + 4 * (vb + 8 * r));
+      vx[sl][r][1] = *reinterpret_cast<const uint32_t*>(vbase + (int64_t)k1 * (D / 2) + 4 * (vb + 8 * r));
     }
   };
-  auto store = [&](int buf) {  // registers -> fp16 (code - zero) in LDS stage buf
-    uint8_t* Ks = smem + buf * GG::STAGE;
+  auto store = [&](auto slot) {  // slot's codes -> fp16 (code - zero) in LDS stage `slot`
+    constexpr int sl = decltype(slot)::value;
+    uint8_t* Ks = smem + sl * GG::STAGE;
     uint8_t* Vs = Ks + GG::KBYTES;
     uint32_t kw[D / 8];
 #pragma unroll
     for (int i = 0; i < GG::KW; ++i) {
-      const uint32_t ws2[2] = {kx[i].x, kx[i].y};
+      const uint32_t ws2[2] = {kx[sl][i].x, kx[sl][i].y};
 #pragma unroll
       for (int hw = 0; hw < 2; ++hw) {
         const uint32_t lo = ws2[hw] & 0x0F0F0F0Fu, hi = (ws2[hw] >> 4) & 0x0F0F0F0Fu;
@@ -166,8 +172,8 @@ __global__ void __launch_bounds__(256) prefill_kernel(const Params p) {
     for (int i = 0; i < D / 32; ++i) kd[i] = make_uint4(kw[4 * i], kw[4 * i + 1], kw[4 * i + 2], kw[4 * i + 3]);
 #pragma unroll
     for (int r = 0; r < GG::VW; ++r) {
-      const uint32_t lo0 = vx[r][0] & 0x0F0F0F0Fu, hi0 = (vx[r][0] >> 4) & 0x0F0F0F0Fu;
-      const uint32_t lo1 = vx[r][1] & 0x0F0F0F0Fu, hi1 = (vx[r][1] >> 4) & 0x0F0F0F0Fu;
+      const uint32_t lo0 = vx[sl][r][0] & 0x0F0F0F0Fu, hi0 = (vx[sl][r][0] >> 4) & 0x0F0F0F0Fu;
+      const uint32_t lo1 = vx[sl][r][1] & 0x0F0F0F0Fu, hi1 = (vx[sl][r][1] >> 4) & 0x0F0F0F0Fu;
 #pragma unroll
       for (int b = 0; b < 4; ++b) {
         const int d = 8 * (vb + 8 * r) + 2 * b;  // dims d (low nibbles) and d + 1 (high nibbles)
@@ -186,15 +192,20 @@ __global__ void __launch_bounds__(256) prefill_kernel(const Params p) {
   float m_run = -INFINITY, l_run = 0.f;
   const float sc = 1.4426950408889634f * __builtin_amdgcn_rsqf((float)D);
 
+  using S0 = std::integral_constant<int, 0>;
+  using S1 = std::integral_constant<int, 1>;
   if (ntiles > 0) {
-    load(0);
-    store(0);
+    load(0, S0{});
+    if (ntiles > 1) load(1, S1{});
+    store(S0{});
   }
   __syncthreads();
-  for (int t = 0; t < ntiles; ++t) {
-    const int buf = t & 1;
-    if (t + 1 < ntiles) load(t + 1);
-    const uint8_t* Ks = smem + buf * GG::STAGE;
+  // iteration t: tile t is in LDS stage t % 2, tile t + 1 in register slot (t + 1) % 2
+  auto iteration = [&](int t, auto slot) {
+    constexpr int sl = decltype(slot)::value;
+    using Next = std::integral_constant<int, sl ^ 1>;
+    if (t + 2 < ntiles) load(t + 2, slot);          // slot sl held tile t, already in LDS
+    const uint8_t* Ks = smem + sl * GG::STAGE;
     const uint8_t* Vs = Ks + GG::KBYTES;
     // S^T: keys 16 n + 4 grp + i of this tile against the lane's query
     floatx4 s[4];
@@ -245,8 +256,12 @@ __global__ void __launch_bounds__(256) prefill_kernel(const Params p) {
         const half4 a = *reinterpret_cast<const half4*>(Vs + (16 * c + col) * GG::VROW + (16 * n + 4 * grp) * 2);
         o[c] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, pb[n], o[c], 0, 0, 0);
       }
-    if (t + 1 < ntiles) store(buf ^ 1);
+    if (t + 1 < ntiles) store(Next{});
     __syncthreads();
+  };
+  for (int t = 0; t < ntiles; t += 2) {
+    iteration(t, S0{});
+    if (t + 1 < ntiles) iteration(t + 1, S1{});
   }
 
   // the 4 lane groups of a column hold disjoint keys: add their sums
