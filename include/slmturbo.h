@@ -167,7 +167,9 @@ int slmt_decode_per_channel(const void* q, const void* k_packed, const void* k_s
  *   q: fp16 [H, M, D]; out: fp32 [H, M, D]; causal masks key n > query m
  *   (both indexed from 0).  block_m/block_n are validated like the reference
  *   (16|32, 32|64, (16,32) only for D != 64) and do not change the result.
- *   workspace: slmt_attention_workspace_bytes(M, H, num_kv_heads, D).
+ *   workspace: slmt_attention_workspace_bytes(M, H, num_kv_heads, D); head_dim
+ *   64 and 128 run on the matrix cores and use none of it (it may be NULL
+ *   there), head_dim 80 needs it.
  */
 int slmt_prefill_per_channel(const void* q, const void* k_packed, const void* k_scale,
                              const void* k_zero, const void* v_packed, const void* v_scale,
