@@ -187,3 +187,29 @@ def test_mixed_shapes_share_workspace():
     refs = [paged_reference(c) for c in cases]
     for i in (0, 1, 2, 0, 2, 1, 0):
         assert_close(_run_batched(cases[i]), refs[i], what=f"case {i}")
+
+
+@pytest.mark.parametrize("D", [64, 128])
+def test_batch_beyond_the_length_stash(D):
+    """300 sequences: the whole-row kernel keeps the first 256 lengths in LDS
+    and reads the rest from memory; lengths 0..40 include empty sequences."""
+    g = torch.Generator().manual_seed(D)
+    lens = torch.randint(0, 41, (300,), generator=g).tolist()
+    case = make_paged_case(seed=D + 1, B=300, H=32, KV=8, D=D, lens=lens)
+    got = _run_batched(case)
+    assert_close(got, paged_reference(case), what=f"B=300 D={D}")
+    assert np.all(got[np.asarray(lens) == 0] == 0.0)
+
+
+@pytest.mark.parametrize("bs,D", [(64, 128), (128, 64), (64, 64)])
+def test_large_block_sizes_whole_row(bs, D):
+    case = make_paged_case(seed=bs + D, B=6, H=32, KV=8, D=D, block_size=bs, len_range=(1, 900))
+    assert_close(_run_batched(case), paged_reference(case), what=f"bs={bs} D={D}")
+
+
+@pytest.mark.parametrize("H,KV,D", [(32, 8, 128), (32, 4, 64)])
+def test_one_long_sequence_over_every_workgroup(H, KV, D):
+    """A single 40K-token sequence: every workgroup holds a piece of it and the
+    merge combines all of them."""
+    case = make_paged_case(seed=H + D, B=1, H=H, KV=KV, D=D, lens=[40000], dist="t3")
+    assert_close(_run_batched(case), paged_reference(case), what=f"one 40K sequence H={H} D={D}")
