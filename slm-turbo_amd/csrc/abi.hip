@@ -256,6 +256,11 @@ int slmt_decode_per_channel(const void* q, const void* k_packed, const void* k_s
   if (rc != SLMT_OK) return rc;
   rc = check_workspace(ph, 1, num_heads, num_kv_heads, head_dim, workspace, workspace_bytes);
   if (rc != SLMT_OK) return rc;
+  // one short sequence: split over (KV head, key chunk) when the shape allows it
+  rc = launch_decode_channel_split(q, k_packed, k_scale, k_zero, v_packed, v_scale, v_zero, num_heads,
+                                   num_heads / num_kv_heads, seq_len, head_dim, use_quant, out, workspace,
+                                   workspace_bytes, reinterpret_cast<hipStream_t>(stream));
+  if (rc != SLMT_ERR_UNSUPPORTED) return rc;
   AttnParams p = blank_params();
   p.q = reinterpret_cast<const uint16_t*>(q);
   p.q_seq_stride = (int64_t)num_heads * head_dim;

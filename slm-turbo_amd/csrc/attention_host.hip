@@ -15,10 +15,7 @@ struct WsLayout {
   int64_t part_o, part_ml, counters, total;
 };
 
-// Arrival counters live in a fixed region at the start of every workspace, so
-// calls of any shape that share a workspace never overwrite each other's
-// counters with partial results (each call leaves its counters at zero).
-constexpr int64_t kCounterCap = int64_t(1) << 20;
+constexpr int64_t kCounterCap = kWsCounterInts;
 
 WsLayout ws_layout(const AttnPlan& pl, int B, int H, int D) {
   auto al = [](int64_t x) { return (x + 255) & ~255LL; };

@@ -219,6 +219,20 @@ int rows_max_workgroups(int D, int nkv, int wpk, int groups, int cus);
 int launch_attention_rows(int D, int nkv, int wpk, int groups, const AttnParams& p, hipStream_t stream);
 int64_t attention_workspace_bytes(int B, int H, int KV, int D);
 
+// Arrival counters live in a fixed region at the start of every workspace, so
+// calls of any shape that share a workspace never overwrite each other's
+// counters with partial results (each call leaves its counters at zero).
+constexpr int64_t kWsCounterInts = int64_t(1) << 20;
+
+// Single-sequence per-channel decode split over (KV head, key chunk)
+// workgroups (decode_channel.hip), head_dim 64 and 128, up to 8 query heads per
+// KV head and 16384 keys.  Returns SLMT_ERR_UNSUPPORTED (without an error
+// message) when the request falls outside that, so the caller can take the
+// general path.
+int launch_decode_channel_split(const void* q, const void* kp, const void* ks, const void* kz, const void* vp,
+                                const void* vs, const void* vz, int H, int G, int S, int D, int use_quant, float* out,
+                                void* workspace, int64_t ws_bytes, hipStream_t stream);
+
 // Per-channel prefill on the matrix cores (prefill_mfma.hip), head_dim 64 and 128;
 // no workspace.  q [H, M, D] fp16, codes [KV_t, S, D/2], rulers [KV_t, D].
 bool prefill_mfma_supported(int D);

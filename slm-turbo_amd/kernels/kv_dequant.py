@@ -24,6 +24,7 @@
 # =============================================================================
 from __future__ import annotations
 
+import contextlib
 import math
 import threading
 
@@ -65,17 +66,34 @@ _ws_lock = threading.Lock()
 _ws_cache: dict = {}
 
 
+# Workspace bytes per (device, B, H, KV, D): the plan depends only on these.
+_need_cache: dict = {}
+
+
 def _workspace(lib, device: torch.device, B: int, H: int, KV: int, D: int) -> tuple[int, int]:
-    need = int(lib.slmt_attention_workspace_bytes(B, H, KV, D))
-    if need < 0:
-        raise RuntimeError(_native.last_error(lib))
+    nkey = (device.index, B, H, KV, D)
+    need = _need_cache.get(nkey)
+    if need is None:
+        need = int(lib.slmt_attention_workspace_bytes(B, H, KV, D))
+        if need < 0:
+            raise RuntimeError(_native.last_error(lib))
+        _need_cache[nkey] = need
     key = (device.index, _stream(device))
-    with _ws_lock:
-        buf = _ws_cache.get(key)
-        if buf is None or buf.numel() < need:
-            buf = torch.zeros(max(need, 1 << 20), dtype=torch.uint8, device=device)
-            _ws_cache[key] = buf
+    buf = _ws_cache.get(key)
+    if buf is None or buf.numel() < need:
+        with _ws_lock:
+            buf = _ws_cache.get(key)
+            if buf is None or buf.numel() < need:
+                buf = torch.zeros(max(need, 1 << 20), dtype=torch.uint8, device=device)
+                _ws_cache[key] = buf
     return buf.data_ptr(), buf.numel()
+
+
+def _on_device(dev: torch.device):
+    """Make ``dev`` current for the call (no switch when it already is)."""
+    if dev.index is None or dev.index == torch.cuda.current_device():
+        return contextlib.nullcontext()
+    return torch.cuda.device(dev)
 
 
 def _require(cond: bool, msg: str) -> None:
@@ -126,7 +144,7 @@ def kv_dequant_decode_attention(
     _check_common(q, k_packed, k_scale, k_zero, v_packed, v_scale, v_zero, phase, num_kv_heads)
     _require(num_kv_heads <= KV, f"{phase}: num_kv_heads {num_kv_heads} exceeds the packed KV heads {KV}")
     dev = q.device
-    with torch.cuda.device(dev):
+    with _on_device(dev):
         out = torch.empty((H, 1, D), dtype=torch.float32, device=dev)
         if S == 0:  # the reference divides 0 by 0
             return out.fill_(math.nan)
@@ -180,7 +198,7 @@ def kv_dequant_prefill_attention(
     _require(q.dim() == 3, f"{phase}: q must be [H, M, D], got {list(q.shape)}")
     _require(num_kv_heads <= KV, f"{phase}: num_kv_heads {num_kv_heads} exceeds the packed KV heads {KV}")
     dev = q.device
-    with torch.cuda.device(dev):
+    with _on_device(dev):
         out = torch.empty((H, M, D), dtype=torch.float32, device=dev)
         if M == 0:
             return out
@@ -229,7 +247,7 @@ def kv_dequant_decode_per_token_attention(
                  f"{phase}: min/step tensors must be fp16 CUDA [KV, S]")
     _require(num_kv_heads <= KV, f"{phase}: num_kv_heads {num_kv_heads} exceeds the packed KV heads {KV}")
     dev = q.device
-    with torch.cuda.device(dev):
+    with _on_device(dev):
         out = torch.empty((H, 1, D), dtype=torch.float32, device=dev)
         if S == 0:
             return out.fill_(math.nan)
@@ -271,7 +289,7 @@ def kv_quantize_store(key, value, kv_cache, slot_mapping, block_size):
     _require(kv_cache.dim() == 4 and kv_cache.size(2) == KV and kv_cache.size(1) == block_size,
              f"store: kv_cache must be [num_blocks, {block_size}, {KV}, {SLOT}], got {list(kv_cache.shape)}")
     dev = key.device
-    with torch.cuda.device(dev):
+    with _on_device(dev):
         # token-strided rows are read in place; anything else is made contiguous
         def rows(t):
             if t.stride(2) == 1 and t.stride(1) == D and t.stride(0) % 2 == 0:
@@ -315,7 +333,7 @@ def kv_dequant_decode_per_token_paged_attention(
     _require(block_table.dtype in (torch.int64, torch.int32), "paged decode: block_table must be int64 or int32")
     seq_len = int(seq_len)
     dev = q.device
-    with torch.cuda.device(dev):
+    with _on_device(dev):
         out = torch.empty((H, 1, D), dtype=torch.float32, device=dev)
         if seq_len <= 0:
             return out.fill_(math.nan)
@@ -368,7 +386,7 @@ def kv_dequant_decode_paged_batched(
     _require(seq_lens.is_cuda and seq_lens.dtype == torch.int32 and seq_lens.numel() == B,
              "paged decode: seq_lens must be an int32 CUDA tensor [B]")
     dev = q.device
-    with torch.cuda.device(dev):
+    with _on_device(dev):
         if out is None:
             out = torch.empty((B, H, D), dtype=out_dtype or torch.float32, device=dev)
         _require(out.dtype in (torch.float32, torch.float16) and tuple(out.shape) == (B, H, D)
@@ -406,7 +424,7 @@ def quantize_per_channel(x):
     _require(x.is_cuda and x.dtype == torch.float16, "quantize: x must be fp16 CUDA")
     _require(S >= 1, "quantize: the sequence axis must not be empty")
     dev = x.device
-    with torch.cuda.device(dev):
+    with _on_device(dev):
         x = x.contiguous()
         packed = torch.empty((KV, S, D // 2), dtype=torch.uint8, device=dev)
         scale = torch.empty((KV, D), dtype=torch.float16, device=dev)

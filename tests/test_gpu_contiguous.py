@@ -214,3 +214,18 @@ def test_decode_per_token_contiguous(H, KV, D, S):
     torch.cuda.synchronize()
     ref = oa.decode_per_token(q.numpy(), kp, kmin, kstep, vp, vmin, vstep)
     assert_close(out.cpu().numpy(), ref, what="per-token decode")
+
+
+# One sequence, head_dim 64 / 128, up to 8 query heads per KV head and 16384
+# keys: the split (KV head, key chunk) kernel; 20000 keys take the general path.
+@pytest.mark.parametrize("H,KV,D,S,outl", [(8, 8, 64, 1, False), (6, 2, 128, 17, True), (24, 8, 64, 5000, False),
+                                           (16, 2, 128, 9000, True), (4, 4, 128, 20000, False),
+                                           (8, 1, 64, 3333, False)])
+def test_decode_per_channel_split_chunks(H, KV, D, S, outl):
+    q, t = _pc_inputs(H + S, H, KV, S, D, outl)
+    kd = _kd()
+    for _ in range(2):                        # the arrival counters must be left at zero
+        out = kd.kv_dequant_decode_attention(q.to(DEV), *[x.to(DEV) for x in t], num_kv_heads=KV)
+        torch.cuda.synchronize()
+        ref = oa.decode_per_channel(q.numpy(), *[x.numpy() for x in t])
+        assert_close(out.cpu().numpy(), ref, what=f"H={H} KV={KV} D={D} S={S}")
