@@ -16,9 +16,10 @@
 // * K enters as its codes n.  The reference's q.k = sum q_d s_d (n_d - z_d), and
 //   sum q_d s_d z_d is the same for every key of a query row, so it cancels in
 //   the softmax and is never formed.
-// * The per-channel K scale folds into the query: q'_d = q_d * s_d in fp32,
-//   split into an fp16 high part and the fp16 rounding of the remainder; two
-//   products per block keep ~22 bits of q'.
+// * The per-channel K scale and the softmax scale log2(e) / sqrt(D) fold into
+//   the query: q'_d = q_d * log2(e) / sqrt(D) * s_d in fp32, split into an fp16
+//   high part and the fp16 rounding of the remainder; two products per block
+//   keep ~22 bits of q'.
 // * V enters as n - zr, zr the zero point rounded and clamped to 0..15 (the
 //   reference quantizer's zero points are such integers), and the finished row
 //   is o_d = s_d * (sum p (n - zr) / l - (z_d - zr_d)) in fp32.
@@ -93,7 +94,9 @@ __global__ void __launch_bounds__(256) prefill_kernel(const Params p) {
   const int ntiles = (kend + BN - 1) / BN;
   const bool quant = p.use_quant != 0;
 
-  // ---- the lane's query column, scaled per channel and split hi / lo (B operand of S^T)
+  // ---- the lane's query column, scaled per channel and by log2(e) / sqrt(D) (so
+  // the scores come out as base-2 logits), split hi / lo (B operand of S^T)
+  const float sc = 1.4426950408889634f * __builtin_amdgcn_rsqf((float)D);
   half8 qh[D / 32], ql[D / 32];
   {
     const uint16_t* qrow = p.q + ((int64_t)h * p.M + mq) * D;
@@ -104,7 +107,7 @@ __global__ void __launch_bounds__(256) prefill_kernel(const Params p) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const int d = 32 * j + 8 * grp + e;
-        float x = hf((uint16_t)(wds[e >> 1] >> (16 * (e & 1))));
+        float x = hf((uint16_t)(wds[e >> 1] >> (16 * (e & 1)))) * sc;
         if (quant) x *= hf(p.ks[(int64_t)kv * D + d]);
         const _Float16 hi = (_Float16)x;
         qh[j][e] = hi;
@@ -190,7 +193,6 @@ __global__ void __launch_bounds__(256) prefill_kernel(const Params p) {
 #pragma unroll
   for (int c = 0; c < D / 16; ++c) o[c] = floatx4{0.f, 0.f, 0.f, 0.f};
   float m_run = -INFINITY, l_run = 0.f;
-  const float sc = 1.4426950408889634f * __builtin_amdgcn_rsqf((float)D);
 
   using S0 = std::integral_constant<int, 0>;
   using S1 = std::integral_constant<int, 1>;
@@ -219,21 +221,40 @@ __global__ void __launch_bounds__(256) prefill_kernel(const Params p) {
         s[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, ql[j], s[n], 0, 0, 0);
       }
     }
+    // Keys past S or past a causal row are masked.  A tile whose keys all lie
+    // before S and at or before the wave's first row (m0 + 16 w) needs no mask:
+    // the test is uniform over the wave.
+    const int kt0 = t * BN;
+    const bool whole = kt0 + BN <= p.S && (!p.causal || kt0 + BN - 1 <= m0 + 16 * w);
     float tmax = -INFINITY;
+    if (whole) {
 #pragma unroll
-    for (int n = 0; n < 4; ++n)
+      for (int n = 0; n < 4; ++n)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int key = t * BN + 16 * n + 4 * grp + i;
-        const bool ok = key < p.S && (!p.causal || key <= m);
-        const float v = ok ? s[n][i] * sc : -INFINITY;
-        s[n][i] = v;
-        tmax = fmaxf(tmax, v);
-      }
+        for (int i = 0; i < 4; ++i) tmax = fmaxf(tmax, s[n][i]);
+    } else {
+#pragma unroll
+      for (int n = 0; n < 4; ++n)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int key = kt0 + 16 * n + 4 * grp + i;
+          const bool ok = key < p.S && (!p.causal || key <= m);
+          const float v = ok ? s[n][i] : -INFINITY;
+          s[n][i] = v;
+          tmax = fmaxf(tmax, v);
+        }
+    }
     tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
     tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
     const float m_new = fmaxf(m_run, tmax);                  // finite: key 0 is visible to every row
-    const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+    // rescale the running sums only when some column's maximum grew (alpha = 0
+    // from the initial -inf, 1 where it did not grow)
+    if (__builtin_amdgcn_ballot_w64(m_new > m_run)) {
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+      l_run *= alpha;
+#pragma unroll
+      for (int c = 0; c < D / 16; ++c) o[c] *= alpha;
+    }
     half4 pb[4];
     float ls = 0.f;
 #pragma unroll
@@ -244,10 +265,8 @@ __global__ void __launch_bounds__(256) prefill_kernel(const Params p) {
         ls += pv;
         pb[n][i] = (_Float16)pv;
       }
-    l_run = l_run * alpha + ls;
+    l_run += ls;
     m_run = m_new;
-#pragma unroll
-    for (int c = 0; c < D / 16; ++c) o[c] *= alpha;
     // O^T: dims 16 c + 4 grp + i
 #pragma unroll
     for (int c = 0; c < D / 16; ++c)
