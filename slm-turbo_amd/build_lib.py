@@ -32,6 +32,9 @@ HIPCC_FLAGS = [
     "-fhip-fp32-correctly-rounded-divide-sqrt",
     # keep hipcc from forming packed-fp32 VALU ops (v_pk_*_f32)
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # matrix-core accumulators in ordinary VGPRs: the softmax reads and rescales
+    # them every tile, which the AGPR form pays for with v_accvgpr copies
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     "-Wall",
 ]
 
