@@ -9,7 +9,7 @@
 // the scores to the output:
 //   S^T = K Q'^T     (v_mfma_f32_16x16x32_f16: A = K rows, B = the lane's query)
 //   P^T = exp2(S^T - m)      (online softmax per query column)
-//   O^T += V^T P^T   (v_mfma_f32_16x16x16f16: B = the lane's P^T block as is)
+//   O^T += V^T P^T   (v_mfma_f32_16x16x32_f16: B = the lane's P^T blocks as they are)
 //
 // Exactness of the operands (a nibble becomes the fp16 1024 + code by one OR with
 // the pattern 0x6400; subtracting an integer below 2048 from it is exact):
@@ -267,13 +267,19 @@ __global__ void __launch_bounds__(256) prefill_kernel(const Params p) {
       }
     l_run += ls;
     m_run = m_new;
-    // O^T: dims 16 c + 4 grp + i
+    // O^T: dims 16 c + 4 grp + i.  One product covers 32 keys: the lane's 8
+    // k slots are keys 32 hh + 4 grp + i and 32 hh + 16 + 4 grp + i (i < 4), the
+    // same keys in the V^T operand (A) and in the weights (B = pb[2 hh], pb[2 hh + 1])
 #pragma unroll
     for (int c = 0; c < D / 16; ++c)
 #pragma unroll
-      for (int n = 0; n < 4; ++n) {
-        const half4 a = *reinterpret_cast<const half4*>(Vs + (16 * c + col) * GG::VROW + (16 * n + 4 * grp) * 2);
-        o[c] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, pb[n], o[c], 0, 0, 0);
+      for (int hh = 0; hh < 2; ++hh) {
+        const uint8_t* vrow = Vs + (16 * c + col) * GG::VROW;
+        const half4 a0 = *reinterpret_cast<const half4*>(vrow + (32 * hh + 4 * grp) * 2);
+        const half4 a1 = *reinterpret_cast<const half4*>(vrow + (32 * hh + 16 + 4 * grp) * 2);
+        const half8 a = __builtin_shufflevector(a0, a1, 0, 1, 2, 3, 4, 5, 6, 7);
+        const half8 b = __builtin_shufflevector(pb[2 * hh], pb[2 * hh + 1], 0, 1, 2, 3, 4, 5, 6, 7);
+        o[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, o[c], 0, 0, 0);
       }
     if (t + 1 < ntiles) store(Next{});
     __syncthreads();
