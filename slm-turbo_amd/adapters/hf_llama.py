@@ -47,16 +47,10 @@ scale is refused.
 from __future__ import annotations
 
 import math
-import sys
 import time
-from pathlib import Path
 from typing import Any, Optional
 
 import torch
-
-_PKG = Path(__file__).resolve().parent.parent
-if str(_PKG) not in sys.path:
-    sys.path.insert(0, str(_PKG))
 
 ATTN_PACKED = "slm_packed_kv"
 ATTN_FP16 = "slm_fp16_eager"

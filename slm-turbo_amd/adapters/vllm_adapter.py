@@ -34,15 +34,9 @@ registering, and the two classes are defined on top of the mixin alone.
 from __future__ import annotations
 
 import logging
-import sys
-from pathlib import Path
 from typing import Any, Optional
 
 import torch
-
-_PKG = Path(__file__).resolve().parent.parent
-if str(_PKG) not in sys.path:
-    sys.path.insert(0, str(_PKG))
 
 logger = logging.getLogger("slm_turbo.vllm_adapter")
 
@@ -119,11 +113,11 @@ class PackedKVAttentionMixin:
             return output.fill_(0)
         q = query[:N]
         if int(attn_metadata.max_query_len) > 1:
-            if self._has_context(attn_metadata):
-                self._chunked_attention(q, kv_cache, attn_metadata, output, N)
-            else:
+            if self._one_first_chunk(attn_metadata):
                 attn_out = self._prefill_attention(q, key[:N], value[:N], kv_cache, attn_metadata)
                 self._store_output(output, attn_out, N)
+            else:
+                self._chunked_attention(q, kv_cache, attn_metadata, output, N)
         else:
             self._decode_attention(q, kv_cache, attn_metadata, output, N)
         return output
@@ -150,18 +144,29 @@ class PackedKVAttentionMixin:
 
     # ---- chunked prefill continuing cached context -------------------------
     @staticmethod
-    def _has_context(attn_metadata) -> bool:
-        """True when some request of a multi-token step attends to tokens of
-        earlier steps: vLLM's host-side max_seq_len exceeds max_query_len."""
+    def _one_first_chunk(attn_metadata) -> bool:
+        """True when a multi-token step is exactly one request's first chunk:
+        one request (``query_start_loc`` has two entries) whose sequence is
+        all query (host-side ``max_seq_len == max_query_len``).  Only then is
+        one causal SDPA over all the step's tokens per-request attention; the
+        reference applies it to every multi-token step (:216-220), where with
+        two requests the later one attends to the earlier one's tokens and a
+        continuation loses its cached context.  Both facts are host-side
+        (a tensor shape and two ints): no device sync.  Metadata without
+        ``query_start_loc``/``max_seq_len`` (the fields the reference reads,
+        :214-218) is taken as one first chunk, as the reference takes it."""
+        qsl = getattr(attn_metadata, "query_start_loc", None)
         max_seq_len = getattr(attn_metadata, "max_seq_len", None)
-        if max_seq_len is None or getattr(attn_metadata, "query_start_loc", None) is None:
-            return False
-        return int(max_seq_len) > int(attn_metadata.max_query_len)
+        if qsl is None or max_seq_len is None:
+            return True
+        return qsl.shape[0] - 1 == 1 and int(max_seq_len) == int(attn_metadata.max_query_len)
 
     def _chunked_attention(self, query, kv_cache, attn_metadata, output, N):
-        """Prefill chunks that continue cached context, and any decode tokens
-        of the same step, over the packed cache (the reference leaves chunked
-        continuation unsupported, adapters/vllm_adapter.py:238-239).  Query
+        """Every multi-token step other than one request's first chunk: first
+        chunks of several requests, chunks that continue cached context and
+        the decode tokens of the same step, over the packed cache (the
+        reference leaves chunked continuation unsupported,
+        adapters/vllm_adapter.py:238-239).  Query
         token i of request r sits at absolute position p = seq_len[r] -
         query_len[r] + (i - query_start[r]) and attends to tokens [0, p] of r,
         all of which this step's do_kv_cache_update has already written.  Each
@@ -324,7 +329,7 @@ class _StandaloneBackend:
 
 
 _classes = _define_vllm_classes() if VLLM_AVAILABLE else None
-if _classes is not None:  # pragma: no cover - needs vLLM
+if _classes is not None:
     QuantizedKVAttentionImpl, QuantizedKVAttentionBackend = _classes
 else:
     QuantizedKVAttentionImpl = _StandaloneImpl
@@ -341,16 +346,16 @@ def _register_custom_backend() -> bool:
         return True
     if not VLLM_AVAILABLE or _classes is None:
         return False
-    try:  # pragma: no cover - needs vLLM
+    try:
         from vllm.v1.attention.backends.registry import AttentionBackendEnum, register_backend
-    except Exception as e:  # pragma: no cover
+    except Exception as e:  # interface drift
         logger.warning("vLLM backend registry not found (%s)", e)
         return False
-    _patch_attention_layer_spec()          # pragma: no cover
-    register_backend(AttentionBackendEnum.CUSTOM, f"{__name__}.QuantizedKVAttentionBackend")  # pragma: no cover
-    _BACKEND_REGISTERED = True             # pragma: no cover
-    logger.info("slm-turbo packed 4-bit KV backend registered as --attention-backend CUSTOM")  # pragma: no cover
-    return True                            # pragma: no cover
+    _patch_attention_layer_spec()
+    register_backend(AttentionBackendEnum.CUSTOM, f"{__name__}.QuantizedKVAttentionBackend")
+    _BACKEND_REGISTERED = True
+    logger.info("slm-turbo packed 4-bit KV backend registered as --attention-backend CUSTOM")
+    return True
 
 
 def register_plugin() -> None:

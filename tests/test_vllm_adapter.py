@@ -218,16 +218,51 @@ def test_chunked_prefill_continuation_is_one_launch():
     assert torch.all(out == 0.5)
 
 
-def test_first_chunks_keep_the_reference_prefill():
-    """Without earlier context the step keeps the reference's SDPA prefill."""
+def test_one_first_chunk_keeps_the_reference_prefill():
+    """One request with no earlier context keeps the reference's SDPA
+    prefill over the chunk's raw K/V."""
     k = _RecordingKernels()
     impl = _impl(kernels=k)
-    meta = _chunk_meta(seq_lens=[4, 3], query_lens=[4, 3], block_table=torch.zeros(2, 1, dtype=torch.int32))
-    q = torch.randn(7, 8, 64)
-    out = torch.zeros(7, 512)
+    meta = _chunk_meta(seq_lens=[4], query_lens=[4], block_table=torch.zeros(1, 1, dtype=torch.int32))
+    q = torch.randn(4, 8, 64)
+    out = torch.zeros(4, 512)
     impl.forward(None, q, q[:, :2], q[:, :2], torch.zeros(2, 16, 2, 72, dtype=torch.uint8), meta, out)
     assert k.decode_calls == []
     assert torch.all(torch.isfinite(out)) and not torch.all(out == 0)
+
+
+def test_several_first_chunks_attend_per_request():
+    """Two first chunks in one step: one causal SDPA over all 7 tokens would
+    let request 1 attend to request 0's tokens, so the step goes through the
+    packed cache, each token over its own request's prefix."""
+    k = _RecordingKernels()
+    impl = _impl(kernels=k)
+    tables = torch.tensor([[3], [5]], dtype=torch.int32)
+    meta = _chunk_meta(seq_lens=[4, 3], query_lens=[4, 3], block_table=tables)
+    q = torch.randn(7, 8, 64).half()
+    out = torch.zeros(7, 512, dtype=torch.float16)
+    impl.forward(None, q, q, q, torch.zeros(6, 16, 2, 72, dtype=torch.uint8), meta, out)
+    assert len(k.decode_calls) == 1
+    c = k.decode_calls[0]
+    assert c["seq_lens"].tolist() == [1, 2, 3, 4, 1, 2, 3]
+    assert c["block_tables"].tolist() == [[3]] * 4 + [[5]] * 3
+
+
+def test_short_continuation_beside_a_longer_first_chunk():
+    """A 10-token first chunk and a request with 6 cached + 2 new tokens:
+    max_seq_len == max_query_len == 10, yet the second request has context.
+    It must attend to its own 6 cached tokens, not to the other request."""
+    k = _RecordingKernels()
+    impl = _impl(kernels=k)
+    tables = torch.tensor([[1], [2]], dtype=torch.int32)
+    meta = _chunk_meta(seq_lens=[10, 8], query_lens=[10, 2], block_table=tables)
+    assert meta.max_seq_len == meta.max_query_len
+    q = torch.randn(12, 8, 64).half()
+    out = torch.zeros(12, 512, dtype=torch.float16)
+    impl.forward(None, q, q, q, torch.zeros(3, 16, 2, 72, dtype=torch.uint8), meta, out)
+    c = k.decode_calls[0]
+    assert c["seq_lens"].tolist() == list(range(1, 11)) + [7, 8]
+    assert c["block_tables"].tolist() == [[1]] * 10 + [[2]] * 2
 
 
 # ---------------------------------------------------------------- on the GPU
@@ -266,17 +301,14 @@ def test_backend_store_is_bit_exact():
     assert np.array_equal(cache.cpu().numpy(), ref)
 
 
-@pytest.mark.gpu
-def test_backend_chunked_prefill_matches_oracle():
-    """Real kernels: chunks of 7 and 12 tokens continuing 300 and 1000 cached
-    tokens, and one decode token, in one step; each query token against the
-    oracle over its own prefix of the packed cache."""
+def _mixed_step_matches_oracle(lens, qlens, seed):
+    """Real kernels: request r has lens[r] tokens in the packed cache, the
+    last qlens[r] of them new in this step; every query token is checked
+    against the oracle over its own request's prefix of the packed cache."""
     H, KV, D = 32, 8, 128
-    lens = [307, 1012, 90]
-    qlens = [7, 12, 1]
-    case = make_paged_case(seed=91, B=3, H=H, KV=KV, D=D, lens=lens)
+    case = make_paged_case(seed=seed, B=len(lens), H=H, KV=KV, D=D, lens=lens)
     N = sum(qlens)
-    g = torch.Generator().manual_seed(92)
+    g = torch.Generator().manual_seed(seed + 1)
     q = torch.randn(N, H, D, generator=g).half()
     # the oracle case: one sequence per query token
     rows, vlens = [], []
@@ -296,4 +328,19 @@ def test_backend_chunked_prefill_matches_oracle():
     out = torch.zeros(N, H * D, dtype=torch.float16, device=dev)
     impl.forward(None, q.to(dev), q.to(dev), q.to(dev), torch.from_numpy(case.kv_cache).to(dev), meta, out)
     torch.cuda.synchronize()
-    assert_close(out.float().cpu().numpy().reshape(N, H, D), ref, atol=3e-3, what="chunked prefill")
+    assert_close(out.float().cpu().numpy().reshape(N, H, D), ref, what="mixed step")
+
+
+@pytest.mark.gpu
+def test_backend_chunked_prefill_matches_oracle():
+    """Chunks of 7 and 12 tokens continuing 300 and 1000 cached tokens, and
+    one decode token, in one step."""
+    _mixed_step_matches_oracle([307, 1012, 90], [7, 12, 1], seed=91)
+
+
+@pytest.mark.gpu
+def test_backend_first_chunks_and_short_continuation_match_oracle():
+    """Two first chunks (10 and 5 tokens) and a continuation of 6 cached
+    tokens by 2 new ones in one step: each request attends to its own tokens
+    only."""
+    _mixed_step_matches_oracle([10, 8, 5], [10, 2, 5], seed=93)
