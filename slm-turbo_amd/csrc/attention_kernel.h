@@ -31,12 +31,14 @@
 //   and read back with readlane, so the loop issues no table loads.
 // * Staging, general path (other layouts): the next tile's 8-byte chunks are
 //   held in registers while the current one is computed, double-buffered.
-// * QK (lane = token p x query head g of the wave's 4 heads): the query is
-//   quantized once per sequence to 16-bit fixed point and split into four
-//   4-bit limbs; v_dot8_u32_u4 multiplies 8 packed key nibbles by 8 limb
-//   nibbles directly, so keys are never unpacked.  q.n = sum_k 16^k dot_k,
-//   offset-corrected with the nibble sum; the per-token affine dequant is
-//   folded in algebraically: q.K = step * q.n + min * sum(q).
+// * QK (lane = token p x query head g of the wave's 4 heads): the fp16 query
+//   is used exactly, scaled by a power of two; each key dword becomes four
+//   fp16 pairs of subnormal integer codes (four masks) that v_dot2c_f32_f16
+//   multiplies exactly with the matching query pairs, accumulating in fp32
+//   (key_pairs / query_pairs below).  The per-token affine dequant is folded
+//   in algebraically: q.K = step * q.n + min * sum(q).  The per-channel
+//   layout multiplies the query by k_scale first and carries the product as
+//   an fp16 pair plus its fp16 remainder (two products per pair).
 // * Softmax: online, base 2 (log2(e)/sqrt(D) folded into the score scale),
 //   per-tile max via DPP row rotations and permlane16/32 swaps.
 // * PV (lane = packed byte j, i.e. dims 2j and 2j+1, for all 4 heads):
@@ -44,7 +46,9 @@
 //   one dword (bytes at bits 0 and 16) and read as an fp16 pair of
 //   subnormals, (lo + 16 hi) * 2^-24, which the instruction multiplies
 //   exactly; a second product with the low nibbles alone (one AND) separates
-//   the two dims.  Weights are p * step in fp16; accumulation is fp32; the
+//   the two dims.  Weights are p * step in fp16; the softmax sums use the
+//   probability each fp16 weight stands for, so the output is an exact
+//   weighted mean of the dequantized rows; accumulation is fp32; the
 //   per-token min enters once per token as sum(p * min).
 #pragma once
 
@@ -57,7 +61,7 @@ namespace attn {
 
 constexpr int TILE = 16;           // tokens per tile, register-staged path
 constexpr int DTILE = 32;          // tokens per tile, direct-load path
-constexpr int WSCR = 1024;         // per-wave LDS scratch bytes (query limbs / weights)
+constexpr int WSCR = 1024;         // per-wave LDS scratch bytes (query pairs / weights)
 constexpr int MAX_THREADS = 512;   // 8 waves: up to 256 VGPRs per wave
 constexpr int MAXP = 5;            // 8-byte chunks prefetched per thread (general path)
 constexpr int DSTAGE = 3;          // LDS ring depth of the direct-load path
@@ -81,6 +85,39 @@ __device__ __forceinline__ float fdot2(uint32_t a, uint32_t b, float c) {
 // Two bytes at bits 0-7 and 16-23 (zero elsewhere): one v_perm_b32.
 __device__ __forceinline__ uint32_t pack_pair(uint32_t b0, uint32_t b1) {
   return __builtin_amdgcn_perm(b1, b0, 0x0C040C00u);
+}
+
+// QK on the exact fp16 query.  A key dword x holds dims 8i..8i+7 (dim 8i+j in
+// nibble j).  Four masks turn it into fp16 pairs of subnormal integers,
+//   (n0, n4), (16 n1, 16 n5), (n2, n6), (16 n3, 16 n7)   (value = bits * 2^-24),
+// and v_dot2c_f32_f16 multiplies each pair exactly with the matching query
+// pair, (q0, q4), (q1/16, q5/16), (q2, q6), (q3/16, q7/16), accumulating in
+// fp32.  The query is first scaled by a power of two so that max|q| lies in
+// [2^14, 2^15): every scaled value and every q/16 is then an fp16 number
+// whose product with a code is exact, and only values below 2^-24 of max|q|
+// lose bits.  The dot is therefore q.n * 2^-24 (scaled) to fp32 accuracy.
+__device__ __forceinline__ void key_pairs(uint32_t x, uint32_t (&P)[4]) {
+  const uint32_t y = x >> 8;
+  P[0] = x & 0x000F000Fu;
+  P[1] = x & 0x00F000F0u;
+  P[2] = y & 0x000F000Fu;
+  P[3] = y & 0x00F000F0u;
+}
+__device__ __forceinline__ uint32_t half_pair(float a, float b) {
+  return (uint32_t)f2h(a) | ((uint32_t)f2h(b) << 16);
+}
+// Query pairs of dims 8i..8i+7 (qs already scaled), in key_pairs' order.
+__device__ __forceinline__ void query_pairs(const float (&qs)[8], uint32_t (&Q)[4]) {
+  Q[0] = half_pair(qs[0], qs[4]);
+  Q[1] = half_pair(qs[1] * 0.0625f, qs[5] * 0.0625f);
+  Q[2] = half_pair(qs[2], qs[6]);
+  Q[3] = half_pair(qs[3] * 0.0625f, qs[7] * 0.0625f);
+}
+// Exponent e such that amax * 2^e lies in [2^14, 2^15) (0 for amax == 0).
+// Scores are then kept as u = step * dot + min * sum(q_scaled) * 2^-24, i.e.
+// q.K * 2^(e - 24), so the base-2 logit is u * log2(e)/sqrt(D) * 2^(24 - e).
+__device__ __forceinline__ int query_exponent(float amax) {
+  return amax > 0.f ? 15 - __builtin_amdgcn_frexp_expf(amax) : 0;
 }
 
 // Workgroup barrier that orders LDS only: global loads issued before it stay
@@ -550,7 +587,7 @@ __host__ __device__ constexpr int dma_split(int D) {   // load holding unit 16*u
 __host__ __device__ constexpr int dma_issues(int D) { return dma_ops(D) + (dma_split(D) >= 0 ? 1 : 0); }
 
 // Per-wave LDS region of the direct-load path: DSTAGE tile stages of
-// dma_ops(D) KB, DSTAGE query slots, the limb/weight scratch; misc follows
+// dma_ops(D) KB, DSTAGE query slots, the query-pair/weight scratch; misc follows
 // the last wave's region.
 struct DmaGeom {
   int stage_bytes, wave_bytes, qslots, wscr, misc, total;
@@ -585,7 +622,11 @@ struct Heads {
   bool hvalid;
   int kvw[4];
   bool hw[4];
-  uint32_t ql[KD][4];
+  // Query pairs of this lane's head for every key dword (key_pairs order);
+  // the per-channel layout folds k_scale into the query, q' = q * s exactly
+  // in fp32, and carries it as an fp16 high part and its fp16 remainder.
+  static constexpr int QP = MODE == SRC_CHANNEL ? 8 : 4;
+  uint32_t qpr[KD][QP];
   float qa, qb, m_run, l_run, vmt;
   float acc[4][2];   // per head: sum w*lo, sum w*(lo + 16 hi), in units of 2^-24
 
@@ -606,8 +647,9 @@ struct Heads {
     jj = min(pj, VB - 1);
   }
 
-  // Start a sequence: quantize the query (qv = this lane's 8 dims; for the
-  // per-channel layout already multiplied by k_scale, zv = k_zero) into limbs.
+  // Start a sequence: scale this lane's 8 query dims (for the per-channel
+  // layout already multiplied by k_scale; zv = k_zero) by the head's power of
+  // two and lay out the query pairs of the head's key dwords.
   __device__ void begin(const float (&qv)[8], const float (&zv)[8], uint8_t* wscr) {
     m_run = -INFINITY;
     l_run = 0.f;
@@ -618,95 +660,83 @@ struct Heads {
 #pragma unroll
     for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(qv[i]));
     amax = red16_max(amax);
-    const float sq = amax > 0.f ? 32767.0f / amax : 1.0f;
-    // The score is computed exactly for the quantized query qi/sq: both the
-    // nibble dot and the ruler terms (sum q, sum q*zero) use qi, so the
-    // quantization error enters as sum(dq * K) with K the dequantized key.
-    uint32_t limb[4] = {0u, 0u, 0u, 0u};
-    int isum = 0;
-    float qzsum = 0.f;
+    const int ex = query_exponent(amax);
+    float qs[8], qsum = 0.f, qzsum = 0.f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      int qi = (int)__builtin_rintf(qv[i] * sq);
-      qi = max(-32767, min(32767, qi));
-      isum += qi;
-      if constexpr (MODE == SRC_CHANNEL) qzsum += (float)qi * zv[i];
-      const uint32_t qu = (uint32_t)(qi + 32768);
-#pragma unroll
-      for (int k = 0; k < 4; ++k) limb[k] |= ((qu >> (4 * k)) & 15u) << (4 * i);
+      qs[i] = __builtin_amdgcn_ldexpf(qv[i], ex);
+      qsum += qs[i];
+      if constexpr (MODE == SRC_CHANNEL) qzsum = __builtin_fmaf(qs[i], zv[i], qzsum);
     }
-    const float qsum = red16_sum((float)isum) / sq;     // |sum qi| < 2^24: exact
-    float zsum = 0.f;
-    if constexpr (MODE == SRC_CHANNEL) zsum = red16_sum(qzsum) / sq;
+    uint32_t pr[8];
+    {
+      uint32_t hp[4];
+      query_pairs(qs, hp);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) pr[k] = hp[k];
+    }
+    if constexpr (MODE == SRC_CHANNEL) {
+      float rs[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) rs[i] = qs[i] - h2f(f2h(qs[i]));   // exact remainder
+      uint32_t lp[4];
+      query_pairs(rs, lp);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) pr[4 + k] = lp[k];
+    }
+    qsum = red16_sum(qsum);
+    if constexpr (MODE == SRC_CHANNEL) qzsum = red16_sum(qzsum);
+    // The table holds 4 pairs per (head, key dword): one pass per group of 4.
     uint32_t* wl = reinterpret_cast<uint32_t*>(wscr);
-    wave_lds_sync();                     // previous tile's weight reads are done
-    if (qp < KD) {
 #pragma unroll
-      for (int k = 0; k < 4; ++k) wl[(qg * 4 + k) * 16 + qp] = limb[k];
+    for (int part = 0; part < QP / 4; ++part) {
+      wave_lds_sync();                   // previous table / weight reads of this wave are done
+      if (qp < KD)
+        *reinterpret_cast<uint4*>(wl + (qg * KD + qp) * 4) =
+            make_uint4(pr[4 * part], pr[4 * part + 1], pr[4 * part + 2], pr[4 * part + 3]);
+      wave_lds_sync();
+#pragma unroll
+      for (int kd = 0; kd < KD; ++kd) {
+        const uint4 v = *reinterpret_cast<const uint4*>(wl + (qg * KD + kd) * 4);
+        qpr[kd][4 * part] = v.x;
+        qpr[kd][4 * part + 1] = v.y;
+        qpr[kd][4 * part + 2] = v.z;
+        qpr[kd][4 * part + 3] = v.w;
+      }
     }
-    wave_lds_sync();
-#pragma unroll
-    for (int kd = 0; kd < KD; ++kd)
-#pragma unroll
-      for (int k = 0; k < 4; ++k) ql[kd][k] = wl[(qg * 4 + k) * 16 + kd];
-    qa = kC / sq;
-    if constexpr (MODE == SRC_CHANNEL) qb = -kC * zsum;
-    else qb = kC * qsum;
+    // base-2 logit = dot * qa + (ruler terms); the dot is in units of 2^-24
+    qa = __builtin_amdgcn_ldexpf(kC, 24 - ex);
+    if constexpr (MODE == SRC_CHANNEL) qb = -__builtin_amdgcn_ldexpf(kC * qzsum, -ex);
+    else qb = __builtin_amdgcn_ldexpf(kC * qsum, -ex);
   }
 
-  // Score of token row `row` of the tile for this lane's head (S_q * q.n
-  // folded with the rulers, base-2 units), and its V ruler for the weights.
+  // Score of token row `row` of the tile for this lane's head (base-2 units),
+  // and its V rulers for the weights.
   __device__ float score(const uint8_t* S, int row_lds, int row, float& vmin, float& vstep) const {
     const uint8_t* kb = S + row * row_lds + kvl * SLOT;
-    uint32_t a0 = 0, a1 = 0, a2 = 0, a3 = 0;
+    float a[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int j = 0; j < KD / 2; ++j) {
       const uint2 w = *reinterpret_cast<const uint2*>(kb + 8 * j);
-      a0 = __builtin_amdgcn_udot8(w.x, ql[2 * j][0], a0, false);
-      a1 = __builtin_amdgcn_udot8(w.x, ql[2 * j][1], a1, false);
-      a2 = __builtin_amdgcn_udot8(w.x, ql[2 * j][2], a2, false);
-      a3 = __builtin_amdgcn_udot8(w.x, ql[2 * j][3], a3, false);
-      a0 = __builtin_amdgcn_udot8(w.y, ql[2 * j + 1][0], a0, false);
-      a1 = __builtin_amdgcn_udot8(w.y, ql[2 * j + 1][1], a1, false);
-      a2 = __builtin_amdgcn_udot8(w.y, ql[2 * j + 1][2], a2, false);
-      a3 = __builtin_amdgcn_udot8(w.y, ql[2 * j + 1][3], a3, false);
-    }
-    // Nibble sum of the token.  When the wave's 4 heads share one KV head the
-    // 4 lanes of the token's quad read the same key, so each sums a quarter
-    // of its dwords and the quad adds the quarters; otherwise every lane sums
-    // its own key.
-    uint32_t sn = 0;
-    if constexpr (SHARED) {
-      const uint2 x0 = *reinterpret_cast<const uint2*>(kb + 16 * qg);
-      const uint2 x1 = *reinterpret_cast<const uint2*>(kb + 16 * qg + 8);
-      const uint32_t xs[4] = {x0.x, x0.y, x1.x, x1.y};
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const uint32_t ones = (KD >= 16 || 4 * qg + i < KD) ? 0x11111111u : 0u;   // key dwords only
-        sn = __builtin_amdgcn_udot8(xs[i], ones, sn, false);
-      }
-      sn += dpp_u<DPP_QUAD_XOR1>(sn);
-      sn += dpp_u<DPP_QUAD_XOR2>(sn);
-    } else {
+      for (int h = 0; h < 2; ++h) {
+        uint32_t P[4];
+        key_pairs(h ? w.y : w.x, P);
 #pragma unroll
-      for (int j = 0; j < KD / 2; ++j) {
-        const uint2 w = *reinterpret_cast<const uint2*>(kb + 8 * j);
-        sn = __builtin_amdgcn_udot8(w.x, 0x11111111u, sn, false);
-        sn = __builtin_amdgcn_udot8(w.y, 0x11111111u, sn, false);
+        for (int k = 0; k < QP; ++k) a[k & 3] = fdot2(P[k & 3], qpr[2 * j + h][k], a[k & 3]);
       }
     }
-    const int iacc = (int)(a0 + (a1 << 4) + (a2 << 8) + (a3 << 12)) - (int)(sn << 15);
-    const float x = (float)iacc;                 // = S_q * (q . n)
+    const float x = (a[0] + a[1]) + (a[2] + a[3]);   // q.n * 2^(e - 24)
     if constexpr (MODE == SRC_CHANNEL) {
       vmin = vstep = 0.f;
-      return x * qa + qb;
+      return __builtin_fmaf(x, qa, qb);
     } else {
       const uint2 rr = *reinterpret_cast<const uint2*>(kb + D);
       const float kmin = h2f((uint16_t)(rr.x & 0xffffu));
       const float kstep = h2f((uint16_t)(rr.x >> 16));
       vmin = h2f((uint16_t)(rr.y & 0xffffu));
       vstep = h2f((uint16_t)(rr.y >> 16));
-      return (x * qa) * kstep + kmin * qb;
+      return __builtin_fmaf(x * qa, kstep, kmin * qb);
     }
   }
 
@@ -741,23 +771,31 @@ struct Heads {
       m_run = m_new;
     }
     const float msafe = (m_run == -INFINITY) ? 0.f : m_run;
-    float wv[NQ];
+    // P.V multiplies the codes by fp16 weights; the softmax sums take the
+    // probability each fp16 weight stands for (per token: w / step, steps
+    // below 2^-10 keep p; per channel: the fp16 p itself), so the output is
+    // an exact weighted mean of the dequantized rows.
+    uint16_t wv[NQ];
 #pragma unroll
     for (int i = 0; i < NQ; ++i) {
-      const float pr = __builtin_amdgcn_exp2f(s2[i] - msafe);
-      l_run += pr;
+      const float pr = __builtin_amdgcn_exp2f(s2[i] - msafe);   // 0 for masked tokens
       if constexpr (MODE == SRC_CHANNEL) {
-        wv[i] = pr;
+        wv[i] = f2h(pr);
+        l_run += h2f(wv[i]);
       } else {
-        wv[i] = tvalid[i] ? pr * vstep[i] : 0.f;
-        vmt += tvalid[i] ? pr * vmin[i] : 0.f;
+        const float st = tvalid[i] ? vstep[i] : 0.f;
+        const float mn = tvalid[i] ? vmin[i] : 0.f;
+        wv[i] = f2h(pr * st);
+        const float pp = st >= 0x1p-10f ? h2f(wv[i]) * __builtin_amdgcn_rcpf(st) : pr;
+        l_run += pp;
+        vmt = __builtin_fmaf(pp, mn, vmt);
       }
     }
     // weights as fp16 pairs: wscr[pair][head] = (w(2i), w(2i+1))
-    wave_lds_sync();                     // limb / weight reads of this wave are done
+    wave_lds_sync();                     // query-pair / weight reads of this wave are done
 #pragma unroll
     for (int i = 0; i < NQ; ++i)
-      reinterpret_cast<uint16_t*>(wscr)[(((qp + 16 * i) >> 1) * 4 + qg) * 2 + (qp & 1)] = f2h(wv[i]);
+      reinterpret_cast<uint16_t*>(wscr)[(((qp + 16 * i) >> 1) * 4 + qg) * 2 + (qp & 1)] = wv[i];
     wave_lds_sync();
     // ---- PV
 #pragma unroll
@@ -976,7 +1014,7 @@ __global__ void __launch_bounds__(MAX_THREADS) attention_kernel(const AttnParams
     }
   };
 
-  // Starts the segment of cursor c: query limbs from its 8 dims.
+  // Starts the segment of cursor c: query pairs from its 8 dims.
   auto begin_segment = [&](const Cursor& c, const uint8_t* qlds) {
     float qv[8], zv[8];
 #pragma unroll

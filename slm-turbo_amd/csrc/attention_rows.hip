@@ -20,11 +20,17 @@
 // publishes the stage, one releases it for the tile after next.
 //
 // QK (lane = token p of 16 x key quarter c of 4; TT/16 rounds per tile): the
-// query is quantized once per sequence to 16-bit fixed point and split into
-// four 4-bit limbs; v_dot8_u32_u4 multiplies 8 packed key nibbles by 8 limb
-// nibbles, so keys are never unpacked.  Each lane dots its quarter of the
-// key with all 4 heads; a reduce-scatter over the quad leaves head c's dot in
-// lane c.  q.K = step * q.n + min * sum(q).
+// fp16 query is used exactly as given (scaled by a power of two).  Each key
+// dword becomes four fp16 pairs of subnormal integer codes with four masks,
+// and v_dot2c_f32_f16 multiplies them exactly by the matching query pairs
+// with fp32 accumulation (key_pairs / query_pairs in attention_kernel.h).
+// Each lane dots its quarter of the key with all 4 heads; a reduce-scatter
+// over the quad leaves head c's dot in lane c.  q.K = step * q.n + min * sum(q).
+//
+// Weights: P.V multiplies the codes by the fp16 weight w = fp16(p * step);
+// the softmax sums use the probability that w stands for, w / step, so the
+// output is an exact weighted mean of the dequantized rows whatever the
+// rounding of w (rows past a sequence's end get weight 0 and rulers 0).
 //
 // PV (lane = V dword column c of 16 x token group g of 4): group g takes the
 // tokens 16m + 4g .. 16m + 4g + 3 of each 16-token round m.  The groups' rows
@@ -78,7 +84,7 @@ struct Shape {
   static constexpr int NP = TT / 8;                       // PV token pairs per lane
   static constexpr int STAGE = TT * RSTRIDE;
   static constexpr int QOFF = NS * STAGE;                 // one 1 KB query slot per wave
-  static constexpr int WOFF = QOFF + WAVES * 1024;        // per-wave query-limb scratch
+  static constexpr int WOFF = QOFF + WAVES * 1024;        // per-wave query-pair table
   static constexpr int MOFF = WOFF + WAVES * 1024;        // misc ints
   static constexpr int STASH = 256;                       // sequence lengths kept in LDS
   static constexpr int SOFF = MOFF + 32 * 4;
@@ -319,15 +325,16 @@ __global__ void __launch_bounds__(NKV * WPK * 64) rows_kernel(const AttnParams p
   auto issue_q = [&](int b) { lds_load16(p.q + (int64_t)b * p.q_seq_stride, qoff, qslot); };
 
   // ---------------------------------------------------------------- per-wave state
-  // QK lane (token p, key quarter qc = lane & 3): limbs of all 4 heads for
-  // the lane's DQ key dwords, in the order the lane reads them (head_dim 128:
-  // odd quarters read their two 8-byte halves swapped, so the quad covers all
-  // 32 banks).  Heads are stored rotated: slot j holds head (qc + j) & 3, so
-  // the quad's reduce-scatter needs no per-lane selects.
-  uint32_t qlq[4][DQ][4];             // [head slot][dword][limb]
-  // Scores are kept in query-integer units, u = step * (qi . n) + min * sum(qi);
-  // qa converts them to base-2 logits (log2(e) / sqrt(D) / query scale), so a
-  // weight is exp2((u - m_run) * qa) and m_run is the running max of u.
+  // QK lane (token p, key quarter qc = lane & 3): query pairs of all 4 heads
+  // for the lane's DQ key dwords, in the order the lane reads them (head_dim
+  // 128: odd quarters read their two 8-byte halves swapped, so the quad
+  // covers all 32 banks).  Heads are stored rotated: slot j holds head
+  // (qc + j) & 3, so the quad's reduce-scatter needs no per-lane selects.
+  uint32_t qpr[4][DQ][4];             // [head slot][dword][pair]
+  // Scores are kept as u = step * dot + min * sum(q) * 2^-24 (q.K in units of
+  // 2^(24 - e), e the query's scale exponent); qa converts them to base-2
+  // logits, so a weight is exp2((u - m_run) * qa) and m_run is the running
+  // max of u.
   float qa = 0.f, qb = 0.f, mq = 0.f, m_run = -INFINITY, l_run = 0.f, vmt = 0.f;
   float accl[DQ][4], accf[DQ][4];     // [byte k][head]: sum w * lo, sum w * (lo + 16 hi), units of 2^-24
   const int pc = lane & 15, pq = lane >> 4;   // PV: V column (DQ bytes), token group
@@ -352,88 +359,67 @@ __global__ void __launch_bounds__(NKV * WPK * 64) rows_kernel(const AttnParams p
 #pragma unroll
     for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(qv[i]));
     amax = red16_max(amax);
-    // scale to 16-bit fixed point; the score below uses the same reciprocal
-    // of it throughout, so it is exact for the quantized query qi * rsq
-    const float sq = amax > 0.f ? 32767.0f * __builtin_amdgcn_rcpf(amax) : 1.0f;
-    const float rsq = __builtin_amdgcn_rcpf(sq);
-    // The nibble dot and sum(q) both use qi.
-    uint32_t limb[4] = {0u, 0u, 0u, 0u};
-    int isum = 0;
+    const int ex = query_exponent(amax);
+    float qs[8], qsum = 0.f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      int qi = (int)__builtin_rintf(qv[i] * sq);
-      qi = max(-32767, min(32767, qi));
-      isum += qi;
-      const uint32_t qu = (uint32_t)(qi + 32768);
-#pragma unroll
-      for (int k = 0; k < 4; ++k) limb[k] |= ((qu >> (4 * k)) & 15u) << (4 * i);
+      qs[i] = __builtin_amdgcn_ldexpf(qv[i], ex);   // exact
+      qsum += qs[i];
     }
-    const float qsum = red16_sum((float)isum);    // |sum qi| < 2^24: exact
+    uint32_t pr[4];
+    query_pairs(qs, pr);
+    qsum = red16_sum(qsum);
+    // table of (head, key dword) pairs: word (h * KDW + i) * 4 + k
+    constexpr int KDW = D / 8;
     uint32_t* wl = reinterpret_cast<uint32_t*>(wscr);
-    wave_lds_sync();                     // earlier limb reads of this wave are done
-#pragma unroll
-    for (int k = 0; k < 4; ++k) wl[(qg * 4 + k) * 16 + qp] = limb[k];
+    wave_lds_sync();                     // earlier table reads of this wave are done
+    if (qp < KDW) *reinterpret_cast<uint4*>(wl + (qg * KDW + qp) * 4) = make_uint4(pr[0], pr[1], pr[2], pr[3]);
     wave_lds_sync();
-    // (head h, limb k) words DQ*qc .. DQ*qc+DQ-1 of this lane's quarter
+    // key dwords DQ*qc .. DQ*qc+DQ-1 of this lane's quarter, in read order
     const bool swp = qg & 1;
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < 4; ++j) {
+      const int h = (qg + j) & 3;
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const int h = (qg + j) & 3;
-        if constexpr (D == 128) {
-          const uint4 v = *reinterpret_cast<const uint4*>(wl + (h * 4 + k) * 16 + 4 * qg);
-          qlq[j][0][k] = swp ? v.z : v.x;
-          qlq[j][1][k] = swp ? v.w : v.y;
-          qlq[j][2][k] = swp ? v.x : v.z;
-          qlq[j][3][k] = swp ? v.y : v.w;
-        } else {
-          const uint2 v = *reinterpret_cast<const uint2*>(wl + (h * 4 + k) * 16 + 2 * qg);
-          qlq[j][0][k] = v.x;
-          qlq[j][1][k] = v.y;
-        }
+      for (int d = 0; d < DQ; ++d) {
+        const int i = DQ * qg + ((D == 128 && swp) ? (d ^ 2) : d);
+        const uint4 v = *reinterpret_cast<const uint4*>(wl + (h * KDW + i) * 4);
+        qpr[j][d][0] = v.x;
+        qpr[j][d][1] = v.y;
+        qpr[j][d][2] = v.z;
+        qpr[j][d][3] = v.w;
       }
-    qa = kC<D> * rsq;
-    qb = qsum;
+    }
+    qa = __builtin_amdgcn_ldexpf(kC<D>, 24 - ex);
+    qb = __builtin_amdgcn_ldexpf(qsum, -24);
   };
 
-  // Score of this lane's token for head qg (base-2 units): the lane's key
-  // quarter kq against all 4 heads' limbs (Horner over the limbs: the dot8
-  // accumulator is shifted by 4 bits between limbs), then the quad's partial
-  // dots for head qg gathered from the rotated slots with three DPP adds;
-  // kr: the token's rulers.
+  // Score u of this lane's token for head qg: the lane's key quarter kq
+  // against all 4 heads' query pairs (exact products, fp32 sums), then the
+  // quad's partial dots for head qg gathered from the rotated slots with
+  // three DPP adds; kr: the token's rulers.
   auto score = [&](const uint32_t (&kq)[DQ], uint2 kr) -> float {
-    uint32_t part[4];
+    float part[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      uint32_t x = 0;
+    for (int d = 0; d < DQ; ++d) {
+      uint32_t P[4];
+      key_pairs(kq[d], P);
 #pragma unroll
-      for (int k = 3; k >= 0; --k) {
-        if (k < 3) x <<= 4;
+      for (int k = 0; k < 4; ++k)
 #pragma unroll
-        for (int d = 0; d < DQ; ++d) x = __builtin_amdgcn_udot8(kq[d], qlq[j][d][k], x, false);
-      }
-      part[j] = x;
+        for (int j = 0; j < 4; ++j) part[j] = fdot2(P[k], qpr[j][d][k], part[j]);
     }
-    // nibble sum of the token: the quad's quarters
-    uint32_t sn = 0;
-#pragma unroll
-    for (int d = 0; d < DQ; ++d) sn = __builtin_amdgcn_udot8(kq[d], 0x11111111u, sn, false);
-    // (the empty asm keeps each DPP move next to a two-operand add, which the
-    // backend then fuses into one v_add_u32_dpp)
-    sn += dpp_u<DPP_QUAD_XOR1>(sn);
-    asm volatile("" : "+v"(sn));
-    sn += dpp_u<DPP_QUAD_XOR2>(sn);
     // lane c: head c lives in slot 0 here, slot 3 of lane c+1, 2 of c+2, 1 of c+3
-    uint32_t z = part[0] + dpp_u<DPP_QUAD_ROT1>(part[3]);
+    // (the empty asm keeps each DPP move next to a two-operand add, which the
+    // backend then fuses into one v_add_f32_dpp)
+    float z = part[0] + dpp_f<DPP_QUAD_ROT1>(part[3]);
     asm volatile("" : "+v"(z));
-    z += dpp_u<DPP_QUAD_XOR2>(part[2]);
+    z += dpp_f<DPP_QUAD_XOR2>(part[2]);
     asm volatile("" : "+v"(z));
-    z += dpp_u<DPP_QUAD_ROT3>(part[1]);
-    const int iacc = (int)z - (int)(sn << 15);
+    z += dpp_f<DPP_QUAD_ROT3>(part[1]);
     const float kmin = h2f((uint16_t)(kr.x & 0xffffu));
     const float kstep = h2f((uint16_t)(kr.x >> 16));
-    return (float)iacc * kstep + kmin * qb;
+    return __builtin_fmaf(z, kstep, kmin * qb);
   };
 
   // PV token pairs of this lane's group: pairs P = 8m + 2pq and 8m + 2pq + 1,
@@ -516,11 +502,22 @@ __global__ void __launch_bounds__(NKV * WPK * 64) rows_kernel(const AttnParams p
     for (int r = 0; r < S::ROUNDS; ++r) {
       // m_run > -inf here: token 0 of every tile is valid
       const float pr = __builtin_amdgcn_exp2f(__builtin_fmaf(s2[r], qa, -mq));
-      const float vmin = h2f((uint16_t)(kr[r].y & 0xffffu));
-      const float vstep = h2f((uint16_t)(kr[r].y >> 16));
-      l_run += pr;
-      vmt = __builtin_fmaf(pr, vmin, vmt);
+      float vmin = h2f((uint16_t)(kr[r].y & 0xffffu));
+      float vstep = h2f((uint16_t)(kr[r].y >> 16));
+      if (nvalid < TT) {
+        // the sequence's last tile: slots past its end may hold anything
+        // (a reused block), so their rulers must not reach the sums
+        const bool ok = 16 * r + qp < nvalid;
+        vmin = ok ? vmin : 0.f;
+        vstep = ok ? vstep : 0.f;
+      }
       const uint32_t wl = f2h(pr * vstep);
+      // P.V applies wl; the sums take the probability it stands for, wl /
+      // step.  Steps below 2^-10 keep pr: there the difference moves the
+      // output by less than 2^-22 of the token's weight.
+      const float pp = vstep >= 0x1p-10f ? h2f((uint16_t)wl) * __builtin_amdgcn_rcpf(vstep) : pr;
+      l_run += pp;
+      vmt = __builtin_fmaf(pp, vmin, vmt);
       W[r] = wl | (dpp_u<DPP_ROW_SHL4>(wl) << 16);   // token qp + 1 is 4 lanes up
     }
   };

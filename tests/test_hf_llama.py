@@ -247,7 +247,7 @@ def test_full_model_configuration():
 @pytest.mark.parametrize("H,KV,D,bs", [(8, 2, 64, 8), (32, 4, 64, 16), (32, 8, 128, 16)])
 def test_hook_steps_on_the_gpu(H, KV, D, bs):
     for T, got, ref in _drive("cuda:0", torch.float16, H=H, KV=KV, D=D, bs=bs):
-        assert_close(got, ref, atol=3e-3, what=f"H={H} KV={KV} D={D} step of {T} tokens")
+        assert_close(got, ref, what=f"H={H} KV={KV} D={D} step of {T} tokens")
 
 
 @pytest.mark.gpu

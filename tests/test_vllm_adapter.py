@@ -282,7 +282,7 @@ def test_backend_decode_matches_oracle_with_vllm_metadata():
     out = torch.zeros(6, H * D, dtype=torch.float16, device=dev)
     impl.forward(None, q, q, q, cache, meta, out)
     torch.cuda.synchronize()
-    assert_close(out.float().cpu().numpy().reshape(6, H, D), ref, atol=3e-3, what="backend decode")
+    assert_close(out.float().cpu().numpy().reshape(6, H, D), ref, what="backend decode")
 
 
 @pytest.mark.gpu
