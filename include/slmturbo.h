@@ -116,6 +116,29 @@ int slmt_decode_paged_batched(const void* q, int64_t q_seq_stride, int64_t q_hea
                               slmt_stream_t stream);
 
 /*
+ * Allocation-free batched paged decode.  No counterpart in the reference: it
+ * is for callers that cannot allocate device memory or pass a workspace (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  Arguments, kernels and results are those of
+ * slmt_decode_paged_batched without the workspace: the library keeps one
+ * static device scratch array of SLMT_NOALLOC_SCRATCH_BYTES per GPU for the
+ * life of the process, and calls whose workspace
+ * (slmt_attention_workspace_bytes) would exceed it fail with
+ * SLMT_ERR_UNSUPPORTED.  All calls on one GPU share that array: calls must be
+ * ordered (one stream, or synchronized); overlapping calls race.  Nothing in
+ * the call allocates.
+ */
+#define SLMT_NOALLOC_SCRATCH_BYTES (16 * 1024 * 1024)
+int slmt_decode_paged_batched_noalloc(const void* q, int64_t q_seq_stride, int64_t q_head_stride,
+                                      const void* kv_cache, int64_t num_blocks, int block_size,
+                                      const void* block_tables, int block_table_bits,
+                                      int64_t block_table_stride, const int32_t* seq_lens,
+                                      int fixed_seq_len, int num_seqs, int num_heads,
+                                      int num_kv_heads, int head_dim, void* out, int out_dtype,
+                                      int64_t out_seq_stride, int64_t out_head_stride,
+                                      slmt_stream_t stream);
+
+/*
  * Paged decode of ONE request.  Replaces
  * kv_dequant_decode_per_token_paged_attention_cuda (reference
  * kernels/kv_dequant_cuda.cu:355-410), bound from kernels/kv_dequant.py:236-257.

@@ -88,6 +88,57 @@ int check_workspace(const char* phase, int B, int H, int KV, int D, const void* 
 }
 
 }  // namespace
+
+int decode_paged_batched(const void* q, int64_t q_seq_stride, int64_t q_head_stride, const void* kv_cache,
+                         int64_t num_blocks, int block_size, const void* block_tables, int block_table_bits,
+                         int64_t block_table_stride, const int32_t* seq_lens, int fixed_seq_len, int num_seqs,
+                         int num_heads, int num_kv_heads, int head_dim, void* out, int out_dtype,
+                         int64_t out_seq_stride, int64_t out_head_stride, void* workspace, int64_t workspace_bytes,
+                         hipStream_t stream, bool clear_counters) {
+  const char* ph = "paged decode";
+  if (!head_dim_ok(head_dim)) return fail(SLMT_ERR_INVALID, "paged decode: head_dim must be 64/80/128, got " + s(head_dim));
+  if (num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads != 0)
+    return fail(SLMT_ERR_INVALID, "H not divisible by num_kv_heads");
+  if (block_size <= 0) return fail(SLMT_ERR_INVALID, "paged decode: block_size must be positive, got " + s(block_size));
+  if (block_table_bits != 32 && block_table_bits != 64)
+    return fail(SLMT_ERR_INVALID, "paged decode: block table must be int32 or int64");
+  if (out_dtype != SLMT_OUT_F32 && out_dtype != SLMT_OUT_F16)
+    return fail(SLMT_ERR_INVALID, "paged decode: out dtype must be fp32 or fp16");
+  if (num_seqs < 0) return fail(SLMT_ERR_INVALID, "paged decode: num_seqs must be >= 0");
+  if (!seq_lens && fixed_seq_len < 0) return fail(SLMT_ERR_INVALID, "paged decode: seq_len must be >= 0");
+  if (num_seqs == 0) return SLMT_OK;
+  if (!q || !kv_cache || !block_tables || !out) return fail(SLMT_ERR_INVALID, "paged decode: null pointer argument");
+  if (!aligned(q, 16) || (q_seq_stride % 8) || (q_head_stride % 8))
+    return fail(SLMT_ERR_INVALID, "paged decode: q must be 16-byte aligned with strides that are multiples of 8");
+  if (!aligned(out, out_dtype == SLMT_OUT_F32 ? 8 : 4) || (out_seq_stride & 1) || (out_head_stride & 1))
+    return fail(SLMT_ERR_INVALID, "paged decode: out must be aligned with even strides");
+  if (!aligned(kv_cache, 8)) return fail(SLMT_ERR_INVALID, "paged decode: kv_cache must be 8-byte aligned");
+  int rc = check_workspace(ph, num_seqs, num_heads, num_kv_heads, head_dim, workspace, workspace_bytes);
+  if (rc != SLMT_OK) return rc;
+  AttnParams p = blank_params();
+  p.q = reinterpret_cast<const uint16_t*>(q);
+  p.q_seq_stride = q_seq_stride;
+  p.q_head_stride = q_head_stride;
+  p.cache = reinterpret_cast<const uint8_t*>(kv_cache);
+  p.block_tables = block_tables;
+  p.bt_stride = block_table_stride;
+  p.bt64 = block_table_bits == 64;
+  p.block_size = block_size;
+  p.block_shift = block_shift_of(block_size);
+  p.cache_kv = num_kv_heads;
+  p.num_blocks = num_blocks;
+  p.seq_lens = seq_lens;
+  p.fixed_len = fixed_seq_len;
+  p.B = num_seqs;
+  p.H = num_heads;
+  p.G = num_heads / num_kv_heads;
+  p.out = out;
+  p.out_f16 = out_dtype == SLMT_OUT_F16;
+  p.out_seq_stride = out_seq_stride;
+  p.out_head_stride = out_head_stride;
+  return launch_attention(SRC_PAGED, head_dim, p, workspace, workspace_bytes, stream, clear_counters);
+}
+
 }  // namespace slmt
 
 using namespace slmt;
@@ -148,48 +199,10 @@ int slmt_decode_paged_batched(const void* q, int64_t q_seq_stride, int64_t q_hea
                               int64_t out_seq_stride, int64_t out_head_stride, void* workspace,
                               int64_t workspace_bytes, slmt_stream_t stream) {
   clear_error();
-  const char* ph = "paged decode";
-  if (!head_dim_ok(head_dim)) return fail(SLMT_ERR_INVALID, "paged decode: head_dim must be 64/80/128, got " + s(head_dim));
-  if (num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads != 0)
-    return fail(SLMT_ERR_INVALID, "H not divisible by num_kv_heads");
-  if (block_size <= 0) return fail(SLMT_ERR_INVALID, "paged decode: block_size must be positive, got " + s(block_size));
-  if (block_table_bits != 32 && block_table_bits != 64)
-    return fail(SLMT_ERR_INVALID, "paged decode: block table must be int32 or int64");
-  if (out_dtype != SLMT_OUT_F32 && out_dtype != SLMT_OUT_F16)
-    return fail(SLMT_ERR_INVALID, "paged decode: out dtype must be fp32 or fp16");
-  if (num_seqs < 0) return fail(SLMT_ERR_INVALID, "paged decode: num_seqs must be >= 0");
-  if (!seq_lens && fixed_seq_len < 0) return fail(SLMT_ERR_INVALID, "paged decode: seq_len must be >= 0");
-  if (num_seqs == 0) return SLMT_OK;
-  if (!q || !kv_cache || !block_tables || !out) return fail(SLMT_ERR_INVALID, "paged decode: null pointer argument");
-  if (!aligned(q, 16) || (q_seq_stride % 8) || (q_head_stride % 8))
-    return fail(SLMT_ERR_INVALID, "paged decode: q must be 16-byte aligned with strides that are multiples of 8");
-  if (!aligned(out, out_dtype == SLMT_OUT_F32 ? 8 : 4) || (out_seq_stride & 1) || (out_head_stride & 1))
-    return fail(SLMT_ERR_INVALID, "paged decode: out must be aligned with even strides");
-  if (!aligned(kv_cache, 8)) return fail(SLMT_ERR_INVALID, "paged decode: kv_cache must be 8-byte aligned");
-  int rc = check_workspace(ph, num_seqs, num_heads, num_kv_heads, head_dim, workspace, workspace_bytes);
-  if (rc != SLMT_OK) return rc;
-  AttnParams p = blank_params();
-  p.q = reinterpret_cast<const uint16_t*>(q);
-  p.q_seq_stride = q_seq_stride;
-  p.q_head_stride = q_head_stride;
-  p.cache = reinterpret_cast<const uint8_t*>(kv_cache);
-  p.block_tables = block_tables;
-  p.bt_stride = block_table_stride;
-  p.bt64 = block_table_bits == 64;
-  p.block_size = block_size;
-  p.block_shift = block_shift_of(block_size);
-  p.cache_kv = num_kv_heads;
-  p.num_blocks = num_blocks;
-  p.seq_lens = seq_lens;
-  p.fixed_len = fixed_seq_len;
-  p.B = num_seqs;
-  p.H = num_heads;
-  p.G = num_heads / num_kv_heads;
-  p.out = out;
-  p.out_f16 = out_dtype == SLMT_OUT_F16;
-  p.out_seq_stride = out_seq_stride;
-  p.out_head_stride = out_head_stride;
-  return launch_attention(SRC_PAGED, head_dim, p, workspace, workspace_bytes, reinterpret_cast<hipStream_t>(stream));
+  return decode_paged_batched(q, q_seq_stride, q_head_stride, kv_cache, num_blocks, block_size, block_tables,
+                              block_table_bits, block_table_stride, seq_lens, fixed_seq_len, num_seqs, num_heads,
+                              num_kv_heads, head_dim, out, out_dtype, out_seq_stride, out_head_stride, workspace,
+                              workspace_bytes, reinterpret_cast<hipStream_t>(stream), false);
 }
 
 int slmt_decode_paged(const void* q, const void* kv_cache, int64_t num_blocks, int block_size,

@@ -17,6 +17,12 @@ struct WsLayout {
 
 constexpr int64_t kCounterCap = kWsCounterInts;
 
+// Zero n ints with plain vector stores (a kernel node, not a memset node, so
+// the call stays capturable in a HIP graph).
+__global__ void __launch_bounds__(256) zero_ints(int* p, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) p[i] = 0;
+}
+
 WsLayout ws_layout(const AttnPlan& pl, int B, int H, int D) {
   auto al = [](int64_t x) { return (x + 255) & ~255LL; };
   WsLayout w;
@@ -117,7 +123,8 @@ int64_t attention_workspace_bytes(int B, int H, int KV, int D) {
   return ws_layout(pl, B, H, D).total;
 }
 
-int launch_attention(int mode, int D, AttnParams& p, void* workspace, int64_t ws_bytes, hipStream_t stream) {
+int launch_attention(int mode, int D, AttnParams& p, void* workspace, int64_t ws_bytes, hipStream_t stream,
+                     bool clear_counters) {
   // Direct loads need a power-of-two block of at least 16 tokens (a tile is
   // then one run of consecutive slots) and a 16-byte aligned cache.
   const bool dma_ok = mode == SRC_PAGED && p.block_shift >= 4 && p.num_blocks < (int64_t(1) << 31) &&
@@ -143,8 +150,15 @@ int launch_attention(int mode, int D, AttnParams& p, void* workspace, int64_t ws
   p.nthreads = pl.waves * 64;
   if (p.min_tiles <= 0) p.min_tiles = 4;
   if (mode == SRC_PAGED && pl.rows) {
-    p.W = pl.W_ws;   // the kernel lowers it to the workgroups the CUs hold
+    p.W = pl.W_ws;   // the kernel lowers it to the workgroups the CUs hold (no counters used)
     return launch_attention_rows(D, pl.rows_nkv, pl.rows_wpk, pl.rows_groups, p, stream);
+  }
+  if (clear_counters) {
+    // the last-arriver merges count pieces in counters[group * B + b]
+    const int64_t n = (int64_t)pl.groups * p.B;
+    const int blocks = (int)std::min<int64_t>((n + 255) / 256, 1024);
+    hipLaunchKernelGGL(zero_ints, dim3(blocks), dim3(256), 0, stream, p.counters, n);
+    if (int rc = check_launch("attention counters")) return rc;
   }
   const dim3 grid(pl.W, pl.groups), block(pl.waves * 64);
   if (mode == SRC_PAGED) {

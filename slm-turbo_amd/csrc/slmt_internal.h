@@ -239,7 +239,18 @@ bool prefill_mfma_supported(int D);
 int launch_prefill_mfma(const void* q, const void* kp, const void* ks, const void* kz, const void* vp, const void* vs,
                         const void* vz, int H, int G, int M, int S, int D, int causal, int use_quant, float* out,
                         hipStream_t stream);
+// clear_counters: zero the arrival counters the launch uses (a fill kernel on
+// the stream, before the decode) instead of relying on the previous call
+// having left them at zero.
 int launch_attention(int mode, int D, AttnParams& p, void* workspace, int64_t ws_bytes,
-                     hipStream_t stream);
+                     hipStream_t stream, bool clear_counters = false);
+
+// Body of slmt_decode_paged_batched (abi.hip) over a given workspace.
+int decode_paged_batched(const void* q, int64_t q_seq_stride, int64_t q_head_stride, const void* kv_cache,
+                         int64_t num_blocks, int block_size, const void* block_tables, int block_table_bits,
+                         int64_t block_table_stride, const int32_t* seq_lens, int fixed_seq_len, int num_seqs,
+                         int num_heads, int num_kv_heads, int head_dim, void* out, int out_dtype,
+                         int64_t out_seq_stride, int64_t out_head_stride, void* workspace, int64_t workspace_bytes,
+                         hipStream_t stream, bool clear_counters);
 
 }  // namespace slmt

@@ -38,6 +38,8 @@ SIGNATURES = {
                                  _vp]),
     "slmt_decode_paged_batched": (_i32, [_vp, _i64, _i64, _vp, _i64, _i32, _vp, _i32, _i64, _p_i32, _i32,
                                          _i32, _i32, _i32, _i32, _vp, _i32, _i64, _i64, _vp, _i64, _vp]),
+    "slmt_decode_paged_batched_noalloc": (_i32, [_vp, _i64, _i64, _vp, _i64, _i32, _vp, _i32, _i64, _p_i32,
+                                                 _i32, _i32, _i32, _i32, _i32, _vp, _i32, _i64, _i64, _vp]),
     "slmt_decode_per_token": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32,
                                      _i32, _p_f32, _vp, _i64, _vp]),
     "slmt_decode_per_channel": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32,
