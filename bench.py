@@ -206,6 +206,34 @@ def read_traffic(w: Workload = WORKLOADS["headline"]):
     return None
 
 
+def cpu_model() -> str:
+    """The host CPU's model name (/proc/cpuinfo), else the platform's machine string."""
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
+
+
+def read_valu(w: Workload = WORKLOADS["headline"]):
+    """VALU wave instructions per decode launch (rocprofv3 SQ_INSTS_VALU, committed
+    summary), or None."""
+    path = ROOT / "profiles" / "paged_decode_valu_counters.txt"
+    if not path.exists():
+        return None
+    for line in path.read_text().splitlines():
+        if line.startswith(f"valu_instructions_per_launch[{w.name}]:"):
+            return int(float(line.split(":", 1)[1]))
+    return None
+
+
+# Issue time of a VALU wave instruction on one SIMD (16 lanes x 4 passes) at the
+# 2.1 GHz shader clock measured under this load, and the SIMDs of an MI355X.
+VALU_CYCLES, LOAD_CLOCK_GHZ, SIMDS = 4, 2.1, 1024
+
+
 def cpu_baseline(lens, tables, q, cache_gpu, out_gpu, budget_s: float, w: Workload = WORKLOADS["headline"]):
     """The reference's CPU torch path (oracle/cpu_path.py) on a bounded sample."""
     import torch
@@ -214,8 +242,8 @@ def cpu_baseline(lens, tables, q, cache_gpu, out_gpu, budget_s: float, w: Worklo
 
     from oracle import cpu_path
 
-    # the host's share for one GPU: OMP_NUM_THREADS when set, never more than the affinity mask
-    cores = min(len(os.sched_getaffinity(0)), int(os.environ.get("OMP_NUM_THREADS") or 16))
+    # every CPU of this process's affinity mask
+    cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
     cache = cache_gpu.cpu()
     qc = q.cpu()
@@ -246,7 +274,7 @@ def cpu_baseline(lens, tables, q, cache_gpu, out_gpu, budget_s: float, w: Worklo
         "sample": f"{len(seqs)} of {B} sequences ({sum(L)} tokens), median of {len(times)} runs, "
                   f"{t * 1e3:.1f} ms/run; fp32 SDPA after fp16-rounded dequant",
         "us_per_sample_step": round(t * 1e6, 1),
-        "cpu_model": platform.processor() or platform.machine(),
+        "cpu_model": cpu_model(),
         "max_abs_diff_vs_gpu": err,
     }
 
@@ -468,7 +496,7 @@ def main(argv=None) -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "int4 codes; int32 (QK) / fp32 (PV) accumulate",
+        "dtype": "int4 codes x fp16 query (QK) and x fp16 weights (PV), fp32 accumulate",
         "data": "synthetic: K,V ~ " + ("Student-t(3)" if w.dist == "t3" else "N(0,1)")
                 + " fp16 quantized into the packed cache; q ~ N(0,1)",
         "config": {
@@ -477,14 +505,7 @@ def main(argv=None) -> int:
             "total_tokens": int(lens.sum()), "algorithmic_bytes": nbytes,
             "rotated_sets": sets, "out_dtype": "fp32",
         },
-        "roofline": {
-            "bound": "hbm",
-            "achieved": round(achieved, 2),
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": read_traffic(w),
-        },
+        "roofline": roofline(nbytes, achieved, w),
         "launch_us": {
             "mean": round(mean_launch, 2),
             "median": round(statistics.median(launch_us), 2),
@@ -499,6 +520,28 @@ def main(argv=None) -> int:
     result["append"] = time_append(kd, caches[-1], tables, lens, w, dev)
     print(json.dumps(result))
     return 0
+
+
+def roofline(nbytes: int, achieved: float, w: Workload) -> dict:
+    """The roofline object: achieved algorithmic GB/s against the HBM peak, the
+    counter-measured HBM bytes, and the two floors of a launch: HBM (bytes at
+    8 TB/s) and VALU issue (SQ_INSTS_VALU wave instructions x 4 cycles over
+    1024 SIMDs at 2.1 GHz).  `binding` names the larger floor."""
+    hbm_floor = nbytes / (HBM_PEAK_GBS * 1e9) * 1e6
+    valu = read_valu(w)
+    valu_floor = valu * VALU_CYCLES / SIMDS / (LOAD_CLOCK_GHZ * 1e9) * 1e6 if valu else None
+    return {
+        "bound": "hbm",
+        "achieved": round(achieved, 2),
+        "peak": HBM_PEAK_GBS,
+        "unit": "GB/s",
+        "frac": round(achieved / HBM_PEAK_GBS, 4),
+        "traffic": read_traffic(w),
+        "hbm_floor_us": round(hbm_floor, 2),
+        "valu_instructions": valu,
+        "valu_floor_us": round(valu_floor, 2) if valu_floor else None,
+        "binding": ("valu" if valu_floor and valu_floor > hbm_floor else "hbm"),
+    }
 
 
 def time_append(kd, cache, tables, lens, w: Workload, dev, calls: int = 200) -> dict:
