@@ -151,6 +151,8 @@ int launch_attention(int mode, int D, AttnParams& p, void* workspace, int64_t ws
   if (p.min_tiles <= 0) p.min_tiles = 4;
   if (mode == SRC_PAGED && pl.rows) {
     p.W = pl.W_ws;   // the kernel lowers it to the workgroups the CUs hold (no counters used)
+    if (mfma_rows_enabled(D, pl.rows_nkv, pl.rows_wpk))
+      return launch_attention_mfma(D, pl.rows_nkv, pl.rows_wpk, pl.rows_groups, p, stream);
     return launch_attention_rows(D, pl.rows_nkv, pl.rows_wpk, pl.rows_groups, p, stream);
   }
   if (clear_counters) {

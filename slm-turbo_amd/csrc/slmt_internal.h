@@ -217,6 +217,10 @@ int plan_attention(int B, int H, int G, int D, int dma_kv, AttnPlan* plan);
 bool rows_shape(int H, int G, int D, int cache_kv, int* nkv, int* wpk, int* groups);
 int rows_max_workgroups(int D, int nkv, int wpk, int groups, int cus);
 int launch_attention_rows(int D, int nkv, int wpk, int groups, const AttnParams& p, hipStream_t stream);
+// Matrix-core variant of the whole-row kernel (attention_mfma.hip): whether it
+// serves a whole-row shape (SLMT_PAGED_DECODE=valu turns it off), and its launch.
+bool mfma_rows_enabled(int D, int nkv, int wpk);
+int launch_attention_mfma(int D, int nkv, int wpk, int groups, const AttnParams& p, hipStream_t stream);
 int64_t attention_workspace_bytes(int B, int H, int KV, int D);
 
 // Arrival counters live in a fixed region at the start of every workspace, so

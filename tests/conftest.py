@@ -27,3 +27,16 @@ def pytest_collection_modifyitems(config, items):
     for item in items:
         if "gpu" in item.keywords:
             item.add_marker(skip)
+
+
+@pytest.fixture(params=["mfma", "valu"])
+def paged_kernel(request, monkeypatch):
+    """Runs a paged-decode test through both whole-row kernels: the matrix-core
+    one (the default) and the vector-ALU one (SLMT_PAGED_DECODE=valu).  The
+    library reads the variable on every call.  Shapes outside the whole-row
+    kernels take the per-wave kernel either way."""
+    if request.param == "valu":
+        monkeypatch.setenv("SLMT_PAGED_DECODE", "valu")
+    else:
+        monkeypatch.delenv("SLMT_PAGED_DECODE", raising=False)
+    return request.param

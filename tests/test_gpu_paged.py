@@ -115,20 +115,20 @@ def _run_batched(case: PagedCase, out_dtype=torch.float32, bt_dtype=torch.int32)
                                     # the same whole-row shapes at head_dim 64
                                     (32, 4, 64), (32, 8, 64), (16, 4, 64), (16, 2, 64), (8, 2, 64),
                                     (24, 6, 64), (64, 16, 64), (48, 6, 64)])
-def test_paged_batched_matches_oracle(H, KV, D):
+def test_paged_batched_matches_oracle(H, KV, D, paged_kernel):
     case = make_paged_case(seed=H * 131 + D, B=5, H=H, KV=KV, D=D, len_range=(1, 700))
     assert_close(_run_batched(case), paged_reference(case), what=f"H={H} KV={KV} D={D}")
 
 
 @pytest.mark.parametrize("bs", [1, 8, 16, 32, 48])
 @pytest.mark.parametrize("D", [64, 128])
-def test_paged_block_sizes(bs, D):
+def test_paged_block_sizes(bs, D, paged_kernel):
     case = make_paged_case(seed=bs, B=4, H=8, KV=2, D=D, block_size=bs, len_range=(1, 300))
     assert_close(_run_batched(case), paged_reference(case), what=f"bs={bs} D={D}")
 
 
 @pytest.mark.parametrize("D", [64, 128])
-def test_paged_edge_lengths_and_formats(D):
+def test_paged_edge_lengths_and_formats(D, paged_kernel):
     """Lengths 0, 1, 15, 16, 17 and a long one; int64 tables; fp16 output."""
     case = make_paged_case(seed=11, B=7, H=32, KV=8, D=D, lens=[0, 1, 15, 16, 17, 3000, 0])
     ref = paged_reference(case)
@@ -190,7 +190,7 @@ def test_mixed_shapes_share_workspace():
 
 
 @pytest.mark.parametrize("D", [64, 128])
-def test_batch_beyond_the_length_stash(D):
+def test_batch_beyond_the_length_stash(D, paged_kernel):
     """300 sequences: the whole-row kernel keeps the first 256 lengths in LDS
     and reads the rest from memory; lengths 0..40 include empty sequences."""
     g = torch.Generator().manual_seed(D)
@@ -202,13 +202,13 @@ def test_batch_beyond_the_length_stash(D):
 
 
 @pytest.mark.parametrize("bs,D", [(64, 128), (128, 64), (64, 64)])
-def test_large_block_sizes_whole_row(bs, D):
+def test_large_block_sizes_whole_row(bs, D, paged_kernel):
     case = make_paged_case(seed=bs + D, B=6, H=32, KV=8, D=D, block_size=bs, len_range=(1, 900))
     assert_close(_run_batched(case), paged_reference(case), what=f"bs={bs} D={D}")
 
 
 @pytest.mark.parametrize("H,KV,D", [(32, 8, 128), (32, 4, 64)])
-def test_one_long_sequence_over_every_workgroup(H, KV, D):
+def test_one_long_sequence_over_every_workgroup(H, KV, D, paged_kernel):
     """A single 40K-token sequence: every workgroup holds a piece of it and the
     merge combines all of them."""
     case = make_paged_case(seed=H + D, B=1, H=H, KV=KV, D=D, lens=[40000], dist="t3")

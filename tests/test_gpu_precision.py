@@ -65,7 +65,7 @@ def _run_paged(case: PagedCase, out_dtype=torch.float32):
 @pytest.mark.parametrize("qmode", QMODES)
 @pytest.mark.parametrize("H,KV,D", [(32, 8, 128), (32, 4, 64), (64, 8, 128), (32, 8, 64), (8, 8, 80),
                                     (12, 3, 128)])
-def test_paged_wide_range_queries(H, KV, D, qmode, dist):
+def test_paged_wide_range_queries(H, KV, D, qmode, dist, paged_kernel):
     case = make_paged_case(seed=3 * H + D, B=3, H=H, KV=KV, D=D, len_range=(200, 1500), dist=dist)
     case.q = _shape_q(case.q, qmode, seed=D + H)
     assert_close(_run_paged(case), paged_reference(case), what=f"H={H} KV={KV} D={D} q={qmode} kv={dist}")
@@ -86,7 +86,7 @@ def _extreme_kv(g, L, KV, D):
 
 @pytest.mark.parametrize("qmode", ["normal", "peak13"])
 @pytest.mark.parametrize("H,KV,D", [(32, 8, 128), (32, 4, 64), (8, 8, 80)])
-def test_paged_extreme_rulers(H, KV, D, qmode):
+def test_paged_extreme_rulers(H, KV, D, qmode, paged_kernel):
     """Rows whose steps are near fp16's smallest subnormal or its largest normal."""
     g = torch.Generator().manual_seed(17 + D)
     lens = [300, 1100, 57]
@@ -105,7 +105,7 @@ def test_paged_extreme_rulers(H, KV, D, qmode):
 
 
 @pytest.mark.parametrize("H,KV,D", [(32, 8, 128), (32, 4, 64), (64, 8, 128), (8, 8, 80)])
-def test_paged_stale_slots_past_the_end(H, KV, D):
+def test_paged_stale_slots_past_the_end(H, KV, D, paged_kernel):
     """Slots a sequence does not own hold 0xFF bytes (NaN rulers): no effect on the output."""
     lens = [1, 15, 17, 63, 65, 700]
     case = make_paged_case(seed=23, B=len(lens), H=H, KV=KV, D=D, lens=lens)
@@ -124,7 +124,7 @@ def test_paged_stale_slots_past_the_end(H, KV, D):
 
 
 @pytest.mark.parametrize("H,KV,D", [(32, 8, 128), (32, 4, 64)])
-def test_paged_fp16_output_at_the_bar(H, KV, D):
+def test_paged_fp16_output_at_the_bar(H, KV, D, paged_kernel):
     """fp16 output within the same 2e-3 / 1e-2 bar (its rounding is inside rel 1e-2)."""
     case = make_paged_case(seed=29, B=4, H=H, KV=KV, D=D, len_range=(1, 2500), dist="t3")
     case.q = _shape_q(case.q, "peak13", seed=3)
