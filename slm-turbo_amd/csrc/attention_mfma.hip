@@ -88,10 +88,18 @@ struct Shape {
 template <int D>
 constexpr float kC = D == 128 ? 1.4426950408889634f / 11.313708498984761f : 1.4426950408889634f / 8.0f;
 
-// Position of token t (0..31 within a token half) in the weight scratch: tokens
-// 8m + 2g + s go to 8g + 2m + s, so the 8 k-slots of PV lane group g (tokens
-// 8m + 2g + s, m < 4, s < 2) are 16 contiguous bytes.
-__device__ __forceinline__ int wpos(int t) { return ((t >> 1) & 3) * 8 + (t >> 3) * 2 + (t & 1); }
+// PV k-slot e (e < 8) of lane group g covers token ktok(g, e) of a 32-token
+// half: 8 m + 4 (g & 1) + 2 (g >> 1) + s for e = 2 m + s.  The rows that the
+// two half-waves read at once (groups 0, 1 and 2, 3) are 4 apart, 16 banks
+// apart with an odd-unit row stride, so the V reads are conflict-free.  wpos
+// is the inverse: the token's position 8 g + e in the weight scratch, so the 8
+// k-slots of a lane group are 16 contiguous bytes.
+__device__ __forceinline__ int ktok(int g, int e) { return 8 * (e >> 1) + 4 * (g & 1) + 2 * (g >> 1) + (e & 1); }
+__device__ __forceinline__ int wpos(int t) {
+  const int u = t & 7;
+  const int g = ((u >> 2) & 1) | (((u >> 1) & 1) << 1);
+  return 8 * g + 2 * (t >> 3) + (u & 1);
+}
 
 template <int D, int NKV, int WPK>
 __global__ void __launch_bounds__(NKV * WPK * 64) mfma_kernel(const AttnParams p) {
@@ -238,6 +246,9 @@ __global__ void __launch_bounds__(NKV * WPK * 64) mfma_kernel(const AttnParams p
   //    PV B / C: column col (head col for col < 4), C rows 4 grp + r.
   const int col = lane & 15, grp = lane >> 4;
   const int hq = col >> 2, lx = col & 3;
+  const int stok = 4 * grp + lx;            // the lane's softmax tokens: 16 rb + stok
+  // first of the 16 dims that k-block kb of lane group grp covers (QK)
+  auto kbase = [&](int kb) { return D == 128 ? 32 * grp + 16 * kb : 16 * grp; };
   const uint8_t* const qsl = smem + S::QOFF + wave * 1024;
 
   v4i qb[KB];                          // B operand: limb lx of head hq's scaled query, k-set grp
@@ -259,8 +270,8 @@ __global__ void __launch_bounds__(NKV * WPK * 64) mfma_kernel(const AttnParams p
     for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
-        // dims 64 kb + 16 grp + 8 u .. + 7
-        const uint4 w = *reinterpret_cast<const uint4*>(qsl + 64 * (8 * kb + 2 * grp + u) + 16 * hq);
+        // dims kbase(kb) + 8 u .. + 7
+        const uint4 w = *reinterpret_cast<const uint4*>(qsl + 64 * ((kbase(kb) >> 3) + u) + 16 * hq);
         const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -319,29 +330,45 @@ __global__ void __launch_bounds__(NKV * WPK * 64) mfma_kernel(const AttnParams p
   // ---------------------------------------------------------------- tile data
   // LDS reads of one tile for this lane: QK A rows (packed), the rulers of the
   // lane's softmax tokens, and the V byte pairs of its PV k-slots.
+  // K: lane (row col, group grp) reads bytes [16 grp, 16 grp + 16) of its row's
+  // codes (head_dim 64: [8 grp, 8 grp + 8)); 8 consecutive rows of an odd-unit
+  // stride start in 8 different 4-bank groups.
+  // V: lane (row col, group grp) reads bytes [4 col, 4 col + 4) (head_dim 64:
+  // [2 col, 2 col + 2)) of the V codes of its 8 k-slot tokens.
   struct TileRegs {
-    uint2 k[RB][KB];
-    uint2 rl[4];
-    uint32_t v16[CB][TH][8];
+    uint32_t k[RB][2 * KB];     // packed codes: k-block kb in words 2 kb, 2 kb + 1
+    uint2 rl[RB];               // rulers of the lane's softmax tokens
+    uint32_t v[TH][8];          // V codes of the k-slots, per token half
   };
   auto read_tile = [&](const uint8_t* Sb, TileRegs& R) {
 #pragma unroll
-    for (int rb = 0; rb < RB; ++rb)
+    for (int rb = 0; rb < RB; ++rb) {
+      const uint8_t* row = Sb + (16 * rb + col) * S::RSTRIDE;
+      if constexpr (D == 128) {
+        // a sub-row starts 8-byte aligned (136-byte slots): two 8-byte halves
+        // (one ds_read2_b64)
+        const uint2 w0 = *reinterpret_cast<const uint2*>(row + 16 * grp);
+        const uint2 w1 = *reinterpret_cast<const uint2*>(row + 16 * grp + 8);
+        R.k[rb][0] = w0.x;
+        R.k[rb][1] = w0.y;
+        R.k[rb][2] = w1.x;
+        R.k[rb][3] = w1.y;
+      } else {
+        const uint2 w = *reinterpret_cast<const uint2*>(row + 8 * grp);
+        R.k[rb][0] = w.x;
+        R.k[rb][1] = w.y;
+      }
+    }
 #pragma unroll
-      for (int kb = 0; kb < KB; ++kb)
-        R.k[rb][kb] = *reinterpret_cast<const uint2*>(Sb + (16 * rb + col) * S::RSTRIDE + 32 * kb + 8 * grp);
+    for (int rb = 0; rb < RB; ++rb) R.rl[rb] = *reinterpret_cast<const uint2*>(Sb + (16 * rb + stok) * S::RSTRIDE + D);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) R.rl[r] = *reinterpret_cast<const uint2*>(Sb + (16 * lx + 4 * grp + r) * S::RSTRIDE + D);
+    for (int th = 0; th < TH; ++th)
 #pragma unroll
-    for (int c = 0; c < CB; ++c)
-#pragma unroll
-      for (int th = 0; th < TH; ++th)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          // k-slot e of lane group grp: token 32 th + 8 (e >> 1) + 2 grp + (e & 1)
-          const int tok = 32 * th + 8 * (e >> 1) + 2 * grp + (e & 1);
-          R.v16[c][th][e] = *reinterpret_cast<const uint16_t*>(Sb + tok * S::RSTRIDE + D / 2 + 32 * c + 2 * col);
-        }
+      for (int e = 0; e < 8; ++e) {
+        const uint8_t* src = Sb + (32 * th + ktok(grp, e)) * S::RSTRIDE + D / 2;
+        if constexpr (D == 128) R.v[th][e] = *reinterpret_cast<const uint32_t*>(src + 4 * col);
+        else R.v[th][e] = *reinterpret_cast<const uint16_t*>(src + 2 * col);
+      }
   };
 
   // QK of one tile: 16 tokens x (head, limb) per row block, exact int32.
@@ -351,7 +378,7 @@ __global__ void __launch_bounds__(NKV * WPK * 64) mfma_kernel(const AttnParams p
       C[rb] = v4i{0, 0, 0, 0};
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb) {
-        const uint32_t x0 = R.k[rb][kb].x, x1 = R.k[rb][kb].y;
+        const uint32_t x0 = R.k[rb][2 * kb], x1 = R.k[rb][2 * kb + 1];
         const v4i a{(int)(x0 & 0x0F0F0F0Fu), (int)((x0 >> 4) & 0x0F0F0F0Fu), (int)(x1 & 0x0F0F0F0Fu),
                     (int)((x1 >> 4) & 0x0F0F0F0Fu)};
         C[rb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, qb[kb], C[rb], 0, 0, 0);
@@ -359,7 +386,10 @@ __global__ void __launch_bounds__(NKV * WPK * 64) mfma_kernel(const AttnParams p
     }
   };
 
-  // Limb combine and quad reduce-scatter: s[r] = Q.n of token 16 lx + 4 grp + r, head hq.
+  // Limb combine and quad reduce-scatter: C[rb][r] of lane x is limb x of token
+  // 16 rb + 4 grp + r; the partner across lane bit 1 takes the other pair of
+  // rows, the partner across bit 0 the other row of the pair, so s[rb] = Q.n of
+  // token 16 rb + stok, head hq, summed over the 4 limbs.
   auto combine = [&](const v4i (&C)[RB], float (&s)[4]) {
     const float lsc = __builtin_amdgcn_ldexpf(1.0f, 8 * lx);
     float f[4][4];
@@ -368,20 +398,20 @@ __global__ void __launch_bounds__(NKV * WPK * 64) mfma_kernel(const AttnParams p
 #pragma unroll
       for (int r = 0; r < 4; ++r) f[rb][r] = (float)C[rb][r] * lsc;
     const bool b1 = lx & 2, b0 = lx & 1;
-    float t[2][4];
+    float t[4][2];
 #pragma unroll
-    for (int k = 0; k < 2; ++k)
+    for (int rb = 0; rb < 4; ++rb)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float keep = b1 ? f[2 + k][r] : f[k][r];
-        const float send = b1 ? f[k][r] : f[2 + k][r];
-        t[k][r] = keep + dpp_f<DPP_QUAD_XOR2>(send);
+      for (int k = 0; k < 2; ++k) {
+        const float keep = b1 ? f[rb][2 + k] : f[rb][k];
+        const float send = b1 ? f[rb][k] : f[rb][2 + k];
+        t[rb][k] = keep + dpp_f<DPP_QUAD_XOR2>(send);
       }
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const float keep = b0 ? t[1][r] : t[0][r];
-      const float send = b0 ? t[0][r] : t[1][r];
-      s[r] = keep + dpp_f<DPP_QUAD_XOR1>(send);
+    for (int rb = 0; rb < 4; ++rb) {
+      const float keep = b0 ? t[rb][1] : t[rb][0];
+      const float send = b0 ? t[rb][0] : t[rb][1];
+      s[rb] = keep + dpp_f<DPP_QUAD_XOR1>(send);
     }
   };
 
@@ -419,7 +449,7 @@ __global__ void __launch_bounds__(NKV * WPK * 64) mfma_kernel(const AttnParams p
       const float kmin = h2f((uint16_t)(R.rl[r].x & 0xffffu));
       const float kstep = h2f((uint16_t)(R.rl[r].x >> 16));
       const float sc = __builtin_fmaf(s[r], kstep, kmin * qs);
-      u[r] = 16 * lx + 4 * grp + r < nvalid ? sc : -INFINITY;
+      u[r] = 16 * r + stok < nvalid ? sc : -INFINITY;
     }
     const float tl = fmaxf(fmaxf(u[0], u[1]), fmaxf(u[2], u[3]));
     if (__builtin_amdgcn_ballot_w64(tl > m_run)) {
@@ -446,7 +476,7 @@ __global__ void __launch_bounds__(NKV * WPK * 64) mfma_kernel(const AttnParams p
       if (nvalid < TT) {
         // the sequence's last tile: slots past its end may hold anything (a
         // reused block), so their rulers must not reach the sums
-        const bool ok = 16 * lx + 4 * grp + r < nvalid;
+        const bool ok = 16 * r + stok < nvalid;
         vmin = ok ? vmin : 0.f;
         vstep = ok ? vstep : 0.f;
       }
@@ -459,11 +489,10 @@ __global__ void __launch_bounds__(NKV * WPK * 64) mfma_kernel(const AttnParams p
       vmt = __builtin_fmaf(pp, vmin, vmt);
       wv[r] = w;
     }
-    // tokens 16 lx + 4 grp + r: token half lx >> 1, local 16 (lx & 1) + 4 grp + r
-    const int tl0 = 16 * (lx & 1) + 4 * grp;
-    uint8_t* wh = wscr + (hq * TT + 32 * (lx >> 1)) * 2;
-    *reinterpret_cast<uint32_t*>(wh + 2 * wpos(tl0)) = wv[0] | (wv[1] << 16);
-    *reinterpret_cast<uint32_t*>(wh + 2 * wpos(tl0 + 2)) = wv[2] | (wv[3] << 16);
+    // token 16 r + stok: token half r >> 1, local 16 (r & 1) + stok
+    uint16_t* wh = reinterpret_cast<uint16_t*>(wscr) + hq * TT;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) wh[32 * (r >> 1) + wpos(16 * (r & 1) + stok)] = (uint16_t)wv[r];
   };
 
   // PV of one tile from its V byte pairs and the weights in the scratch.
@@ -482,8 +511,10 @@ __global__ void __launch_bounds__(NKV * WPK * 64) mfma_kernel(const AttnParams p
         uint32_t el[4], eh[4], ol[4], oh[4];
 #pragma unroll
         for (int d = 0; d < 4; ++d) {
-          // [E_t, O_t, E_t', O_t'] of the k-slot pair 2d, 2d + 1
-          const uint32_t x = __builtin_amdgcn_perm(R.v16[c][th][2 * d + 1], R.v16[c][th][2 * d], 0x05040100u);
+          // [E_t, O_t, E_t', O_t'] of the k-slot pair 2d, 2d + 1: bytes 2c, 2c + 1
+          // of the two tokens' V words
+          const uint32_t x = __builtin_amdgcn_perm(R.v[th][2 * d + 1], R.v[th][2 * d],
+                                                   c == 0 ? 0x05040100u : 0x07060302u);
           const uint32_t y = x >> 8;
           el[d] = x & 0x000F000Fu;
           eh[d] = x & 0x00F000F0u;
@@ -501,8 +532,9 @@ __global__ void __launch_bounds__(NKV * WPK * 64) mfma_kernel(const AttnParams p
 
   // End of a segment of sequence b whose first tile is seg_first (a whole
   // sequence when `whole`): write the output or a partial piece.  Lane (col <
-  // 4, grp) holds head col, dims 64 c + 16 grp + 4 r + (0: E.lo, 1: E.hi, 2:
-  // O.lo, 3: O.hi).
+  // 4, grp) holds head col and C row i = 4 grp + r of block c, i.e. V bytes
+  // 4 i + 2 c (E) and 4 i + 2 c + 1 (O) (head_dim 64: 2 i, 2 i + 1), dims
+  // 8 i + 4 c + (0: E.lo, 1: E.hi, 2: O.lo, 3: O.hi) (head_dim 64: 4 i + ...).
   auto finish = [&](int b, int seg_first, bool whole, bool last_of_seq) {
     const float lt = for_pv_lane(head_sum(l_run));
     const float vt = for_pv_lane(head_sum(vmt));
@@ -522,7 +554,7 @@ __global__ void __launch_bounds__(NKV * WPK * 64) mfma_kernel(const AttnParams p
         o[1] = acc[c][1][r] * 1048576.0f + vt;    // (16 n) 2^-24 -> n
         o[2] = acc[c][2][r] * 16777216.0f + vt;
         o[3] = acc[c][3][r] * 1048576.0f + vt;
-        const int d = 64 * c + 16 * grp + 4 * r;
+        const int d = (D == 128 ? 8 : 4) * (4 * grp + r) + 4 * c;
         if (final_out) {
           const int64_t off = (int64_t)b * p.out_seq_stride + (int64_t)h * p.out_head_stride + d;
           if (p.out_f16) {
@@ -581,8 +613,6 @@ __global__ void __launch_bounds__(NKV * WPK * 64) mfma_kernel(const AttnParams p
     }
     TileRegs R;
     read_tile(smem + st * S::STAGE + kvw * SLOT, R);
-    v4i C[RB];
-    qk(R, C);
     lds_barrier();
     // tile t+2 into this stage, in three parts spread over the rest of the
     // iteration
@@ -600,6 +630,8 @@ __global__ void __launch_bounds__(NKV * WPK * 64) mfma_kernel(const AttnParams p
       sinfo[st] = nx.info;
       loads(nx, IC0{}, IC1{});
     }
+    v4i C[RB];
+    qk(R, C);
     float s[4];
     combine(C, s);
     if (more) loads(nx, IC1{}, IC2{});
