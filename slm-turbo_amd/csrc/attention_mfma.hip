@@ -535,42 +535,67 @@ __global__ void __launch_bounds__(NKV * WPK * 64) mfma_kernel(const AttnParams p
   // 4, grp) holds head col and C row i = 4 grp + r of block c, i.e. V bytes
   // 4 i + 2 c (E) and 4 i + 2 c + 1 (O) (head_dim 64: 2 i, 2 i + 1), dims
   // 8 i + 4 c + (0: E.lo, 1: E.hi, 2: O.lo, 3: O.hi) (head_dim 64: 4 i + ...).
+  // The stores are issued one iteration later (flush, right after that
+  // iteration's wait for its tile): stores count in the same in-order vector
+  // memory counter as the tile loads, and stores issued behind tile t+2's loads
+  // would make the next wait hold for those loads too.
+  float ov[CB][4][4];
+  float2 pml = make_float2(0.f, 0.f);
+  int pk = 0;                          // pending stores: 0 none, 1 output, 2 partial piece
+  int64_t pofs = 0, pmlofs = 0;
   auto finish = [&](int b, int seg_first, bool whole, bool last_of_seq) {
     const float lt = for_pv_lane(head_sum(l_run));
     const float vt = for_pv_lane(head_sum(vmt));
     const float mt = for_pv_lane(m_run * qa);
-    if (col >= 4) return;
-    const int h = hw + col;
+    const int h = hw + (col & 3);      // lanes col >= 4 hold no output
     const bool final_out = whole && last_of_seq;
-    const float rL = __builtin_amdgcn_rcpf(lt);
-    const int slot = (seg_first == lo) ? 0 : 1;
-    const int64_t pbase = ((int64_t)wg * 2 + slot) * p.H;
+    const float rL = final_out ? __builtin_amdgcn_rcpf(lt) : 1.0f;
 #pragma unroll
     for (int c = 0; c < CB; ++c)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        float o[4];
-        o[0] = acc[c][0][r] * 16777216.0f + vt;   // 2^24: nibble-as-subnormal scale
-        o[1] = acc[c][1][r] * 1048576.0f + vt;    // (16 n) 2^-24 -> n
-        o[2] = acc[c][2][r] * 16777216.0f + vt;
-        o[3] = acc[c][3][r] * 1048576.0f + vt;
-        const int d = (D == 128 ? 8 : 4) * (4 * grp + r) + 4 * c;
-        if (final_out) {
-          const int64_t off = (int64_t)b * p.out_seq_stride + (int64_t)h * p.out_head_stride + d;
-          if (p.out_f16) {
-            uint2 v;
-            v.x = (uint32_t)f2h(o[0] * rL) | ((uint32_t)f2h(o[1] * rL) << 16);
-            v.y = (uint32_t)f2h(o[2] * rL) | ((uint32_t)f2h(o[3] * rL) << 16);
-            *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(p.out) + off) = v;
-          } else {
-            *reinterpret_cast<float4*>(reinterpret_cast<float*>(p.out) + off) =
-                make_float4(o[0] * rL, o[1] * rL, o[2] * rL, o[3] * rL);
-          }
-        } else {
-          *reinterpret_cast<float4*>(p.part_o + (pbase + h) * D + d) = make_float4(o[0], o[1], o[2], o[3]);
-        }
+        ov[c][r][0] = (acc[c][0][r] * 16777216.0f + vt) * rL;   // 2^24: nibble-as-subnormal scale
+        ov[c][r][1] = (acc[c][1][r] * 1048576.0f + vt) * rL;    // (16 n) 2^-24 -> n
+        ov[c][r][2] = (acc[c][2][r] * 16777216.0f + vt) * rL;
+        ov[c][r][3] = (acc[c][3][r] * 1048576.0f + vt) * rL;
       }
-    if (!final_out && grp == 0) *reinterpret_cast<float2*>(p.part_ml + (pbase + h) * 2) = make_float2(mt, lt);
+    if (final_out) {
+      pk = 1;
+      pofs = (int64_t)b * p.out_seq_stride + (int64_t)h * p.out_head_stride;
+    } else {
+      const int slot = (seg_first == lo) ? 0 : 1;
+      const int64_t pbase = ((int64_t)wg * 2 + slot) * p.H;
+      pk = 2;
+      pofs = (pbase + h) * D;
+      pmlofs = (pbase + h) * 2;
+      pml = make_float2(mt, lt);
+    }
+  };
+  auto flush = [&]() {
+    if (pk == 0) return;
+    if (col < 4) {
+#pragma unroll
+      for (int c = 0; c < CB; ++c)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int d = (D == 128 ? 8 : 4) * (4 * grp + r) + 4 * c;
+          const float* o = ov[c][r];
+          if (pk == 1) {
+            if (p.out_f16) {
+              uint2 v;
+              v.x = (uint32_t)f2h(o[0]) | ((uint32_t)f2h(o[1]) << 16);
+              v.y = (uint32_t)f2h(o[2]) | ((uint32_t)f2h(o[3]) << 16);
+              *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(p.out) + pofs + d) = v;
+            } else {
+              *reinterpret_cast<float4*>(reinterpret_cast<float*>(p.out) + pofs + d) = make_float4(o[0], o[1], o[2], o[3]);
+            }
+          } else {
+            *reinterpret_cast<float4*>(p.part_o + pofs + d) = make_float4(o[0], o[1], o[2], o[3]);
+          }
+        }
+      if (pk == 2 && grp == 0) *reinterpret_cast<float2*>(p.part_ml + pmlofs) = pml;
+    }
+    pk = 0;
   };
 
   // ---------------------------------------------------------------- pipeline
@@ -585,8 +610,9 @@ __global__ void __launch_bounds__(NKV * WPK * 64) mfma_kernel(const AttnParams p
   //   tile t+2 (after the query rows of tile t+1 when that starts a segment);
   //   combine, softmax, PV, and the end of a segment that ends at tile t.
   // The loads of one tile are followed by at most the next tile's query load
-  // and loads (partial stores of a segment end only make the wait stricter),
-  // so waiting until NOPS operations remain covers tile t and its query.
+  // and loads (and output stores, issued behind no later load, which only
+  // make the wait stricter), so waiting until NOPS operations remain covers
+  // tile t and its query.
   build(lo);
   int sinfo[2];
   issue_q(rng.b);
@@ -601,6 +627,7 @@ __global__ void __launch_bounds__(NKV * WPK * 64) mfma_kernel(const AttnParams p
     if (t + 1 < hi) vm_wait_n<S::NOPS>();
     else vm_wait_n<0>();
     lds_barrier();
+    flush();
     const int info = sinfo[st];
     const bool first_of_seq = (info >> 7) & 1;
     const bool seg_start = t == lo || first_of_seq;
@@ -645,6 +672,7 @@ __global__ void __launch_bounds__(NKV * WPK * 64) mfma_kernel(const AttnParams p
     iteration(t, std::integral_constant<int, 0>{});
     if (t + 1 < hi) iteration(t + 1, std::integral_constant<int, 1>{});
   }
+  flush();
   // Split sequences are merged, and empty sequences zeroed, by merge_kernel,
   // launched after this kernel on the same stream.
 }
@@ -659,12 +687,14 @@ __global__ void __launch_bounds__(128) merge_kernel(const AttnParams p) {
   constexpr int TT = 64;
   const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int h0 = blockIdx.y * MH, h1 = min(p.H, h0 + MH);
-  __shared__ int red[4];
+  __shared__ int red[5];
   int pre = 0, tot = 0;
   for (int i = tid; i < p.B; i += blockDim.x) {
-    const int t = tiles_of<TT>(seq_len_lane(p, i));
+    const int Li = seq_len_lane(p, i);
+    const int t = tiles_of<TT>(Li);
     tot += t;
     pre += i < b ? t : 0;
+    if (i == b) red[4] = Li;   // the sequence's own length, from the same loads
   }
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) {
@@ -677,7 +707,7 @@ __global__ void __launch_bounds__(128) merge_kernel(const AttnParams p) {
   }
   __syncthreads();
   const int Pb = red[0] + red[1], T = red[2] + red[3];
-  const int L = seq_len_of(p, b);
+  const int L = red[4];
   if (L == 0) {
     for (int e = tid; e < (h1 - h0) * D; e += blockDim.x) {
       const int64_t o = (int64_t)b * p.out_seq_stride + (int64_t)(h0 + e / D) * p.out_head_stride + e % D;
