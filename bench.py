@@ -18,7 +18,8 @@ untimed for --prewarm-ms (default 100 ms); the JSON line reports it.
 Printed: one JSON line with the throughput in algorithmic GB/s (packed KV +
 rulers, q, fp32 out, block-table entries and lengths actually read) over K
 back-to-back steps, the time per step, the roofline object for the decode
-kernel (its duration from an event pair around each of K further launches) and
+kernel (its own duration from a HIP event pair stamped from its dispatch on the
+launch stream, slmt_kernel_timing, over K further launches) and
 a CPU baseline (the reference's CPU torch path on a bounded sample of the same
 workload).
 
@@ -48,6 +49,7 @@ hook in slm-turbo_amd/adapters/hf_llama.py).
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
 import platform
@@ -217,21 +219,23 @@ def cpu_model() -> str:
     return platform.processor() or platform.machine()
 
 
-def read_valu(w: Workload = WORKLOADS["headline"]):
-    """VALU wave instructions per decode launch (rocprofv3 SQ_INSTS_VALU, committed
-    summary), or None."""
+def read_counter(key: str, w: Workload = WORKLOADS["headline"]):
+    """Per-launch instruction count `key` (valu_instructions_per_launch or
+    mfma_instructions_per_launch, rocprofv3 SQ_INSTS_VALU / SQ_INSTS_MFMA) from
+    the committed counter summary, or None."""
     path = ROOT / "profiles" / "paged_decode_valu_counters.txt"
     if not path.exists():
         return None
     for line in path.read_text().splitlines():
-        if line.startswith(f"valu_instructions_per_launch[{w.name}]:"):
+        if line.startswith(f"{key}[{w.name}]:"):
             return int(float(line.split(":", 1)[1]))
     return None
 
 
-# Issue time of a VALU wave instruction on one SIMD (16 lanes x 4 passes) at the
-# 2.1 GHz shader clock measured under this load, and the SIMDs of an MI355X.
-VALU_CYCLES, LOAD_CLOCK_GHZ, SIMDS = 4, 2.1, 1024
+# Issue time of a VALU wave instruction on one SIMD (16 lanes x 4 passes) and of
+# the 16x16x64 int8 / 16x16x32 fp16 MFMA instructions, at the 2.1 GHz shader
+# clock measured under this load, and the SIMDs of an MI355X.
+VALU_CYCLES, MFMA_CYCLES, LOAD_CLOCK_GHZ, SIMDS = 4, 16, 2.1, 1024
 
 
 def cpu_baseline(lens, tables, q, cache_gpu, out_gpu, budget_s: float, w: Workload = WORKLOADS["headline"]):
@@ -469,19 +473,33 @@ def main(argv=None) -> int:
     t_end.record(stream)
     torch.cuda.synchronize()
     total_ms = t_start.elapsed_time(t_end)
+    # During these K steps the library also times the decode kernel alone
+    # (slmt_kernel_timing: a HIP event pair stamped from the kernel's dispatch on
+    # the launch stream); its duration, without the merge kernel that follows
+    # it, is the roofline's.
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(K)]
+    _native.check(lib, lib.slmt_kernel_timing(1))
     for i in range(K):
         ev[i][0].record(stream)
         fn(*argsets[i % sets])
         ev[i][1].record(stream)
     torch.cuda.synchronize()
+    lib.slmt_kernel_timing(0)
+    kbuf = (ctypes.c_float * K)()
+    nk = lib.slmt_kernel_timing_read(kbuf, K)
+    if nk < 0:
+        raise RuntimeError("kernel timing: " + _native.last_error(lib))
+    kernel_us = sorted(kbuf[:nk])
     launch_us = sorted(a.elapsed_time(b) * 1e3 for a, b in ev)
 
     nbytes = algorithmic_bytes(lens, w)
     ms_per_step = total_ms / K
     value = nbytes / (ms_per_step * 1e-3) / 1e9
     mean_launch = statistics.fmean(launch_us)
-    achieved = nbytes / (mean_launch * 1e-6) / 1e9
+    # the dominant kernel's own duration (the whole-row decode); calls that
+    # take another kernel record none, and then the whole call is used
+    mean_kernel = statistics.fmean(kernel_us) if kernel_us else mean_launch
+    achieved = nbytes / (mean_kernel * 1e-6) / 1e9
     result = {
         "metric": w.metric,
         "value": round(value, 2),
@@ -506,11 +524,19 @@ def main(argv=None) -> int:
             "rotated_sets": sets, "out_dtype": "fp32",
         },
         "roofline": roofline(nbytes, achieved, w),
+        "kernel_us": ({
+            "mean": round(mean_kernel, 2),
+            "median": round(statistics.median(kernel_us), 2),
+            "p10": round(kernel_us[len(kernel_us) // 10], 2),
+            "p90": round(kernel_us[(9 * len(kernel_us)) // 10], 2),
+            "note": "decode kernel alone: HIP events stamped from its dispatch (slmt_kernel_timing)",
+        } if kernel_us else None),
         "launch_us": {
             "mean": round(mean_launch, 2),
             "median": round(statistics.median(launch_us), 2),
             "p10": round(launch_us[len(launch_us) // 10], 2),
             "p90": round(launch_us[(9 * len(launch_us)) // 10], 2),
+            "note": "whole call (decode + merge kernels) inside an event pair",
         },
     }
     if not args.no_cpu:
@@ -524,12 +550,18 @@ def main(argv=None) -> int:
 
 def roofline(nbytes: int, achieved: float, w: Workload) -> dict:
     """The roofline object: achieved algorithmic GB/s against the HBM peak, the
-    counter-measured HBM bytes, and the two floors of a launch: HBM (bytes at
-    8 TB/s) and VALU issue (SQ_INSTS_VALU wave instructions x 4 cycles over
-    1024 SIMDs at 2.1 GHz).  `binding` names the larger floor."""
+    counter-measured HBM bytes, and three floors of a launch: HBM (bytes at
+    8 TB/s), VALU issue (SQ_INSTS_VALU wave instructions x 4 cycles over 1024
+    SIMDs at 2.1 GHz) and matrix cores (SQ_INSTS_MFMA x 16 cycles over 1024
+    SIMDs at 2.1 GHz; both MFMA shapes used are 16-cycle instructions).
+    `binding` names the largest floor."""
     hbm_floor = nbytes / (HBM_PEAK_GBS * 1e9) * 1e6
-    valu = read_valu(w)
-    valu_floor = valu * VALU_CYCLES / SIMDS / (LOAD_CLOCK_GHZ * 1e9) * 1e6 if valu else None
+    valu = read_counter("valu_instructions_per_launch", w)
+    mfma = read_counter("mfma_instructions_per_launch", w)
+    clock = LOAD_CLOCK_GHZ * 1e9
+    valu_floor = valu * VALU_CYCLES / SIMDS / clock * 1e6 if valu else None
+    mfma_floor = mfma * MFMA_CYCLES / SIMDS / clock * 1e6 if mfma else None
+    floors = {"hbm": hbm_floor, "valu": valu_floor or 0.0, "mfma": mfma_floor or 0.0}
     return {
         "bound": "hbm",
         "achieved": round(achieved, 2),
@@ -540,7 +572,9 @@ def roofline(nbytes: int, achieved: float, w: Workload) -> dict:
         "hbm_floor_us": round(hbm_floor, 2),
         "valu_instructions": valu,
         "valu_floor_us": round(valu_floor, 2) if valu_floor else None,
-        "binding": ("valu" if valu_floor and valu_floor > hbm_floor else "hbm"),
+        "mfma_instructions": mfma,
+        "mfma_floor_us": round(mfma_floor, 2) if mfma_floor else None,
+        "binding": max(floors, key=floors.get),
     }
 
 

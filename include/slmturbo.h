@@ -202,6 +202,21 @@ int slmt_prefill_per_channel(const void* q, const void* k_packed, const void* k_
                              float* out, void* workspace, int64_t workspace_bytes,
                              slmt_stream_t stream);
 
+/*
+ * Measurement hook; it has no counterpart in the reference and is for
+ * benchmark harnesses (bench.py).  slmt_kernel_timing(1) makes each following
+ * batched paged decode call that runs a whole-row kernel time that kernel
+ * alone (not the merge of split sequences that follows it) with a HIP event
+ * pair stamped from the kernel's own dispatch (hipExtLaunchKernelGGL), for up
+ * to 4096 calls; slmt_kernel_timing(0) stops.  The events are created when
+ * timing is first switched on (on the device current then), so a timed call
+ * creates nothing.  slmt_kernel_timing_read waits for the recorded events,
+ * writes up to max_n durations in microseconds (call order) to us, forgets
+ * all recorded pairs and returns how many it wrote, or -1 on a HIP error.
+ */
+int slmt_kernel_timing(int enable);
+int slmt_kernel_timing_read(float* us, int max_n);
+
 #ifdef __cplusplus
 }
 #endif

@@ -346,4 +346,15 @@ int slmt_prefill_per_channel(const void* q, const void* k_packed, const void* k_
   return launch_attention(SRC_CHANNEL, head_dim, p, workspace, workspace_bytes, reinterpret_cast<hipStream_t>(stream));
 }
 
+int slmt_kernel_timing(int enable) {
+  clear_error();
+  return set_kernel_timing(enable != 0);
+}
+
+int slmt_kernel_timing_read(float* us, int max_n) {
+  clear_error();
+  if (us == nullptr && max_n > 0) return fail(SLMT_ERR_INVALID, "timing: output array is null"), -1;
+  return read_kernel_timing(us, max_n);
+}
+
 }  // extern "C"

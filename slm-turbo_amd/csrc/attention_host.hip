@@ -3,8 +3,76 @@
 #include "attention_kernel.h"
 
 #include <algorithm>
+#include <mutex>
+#include <utility>
+#include <vector>
 
 namespace slmt {
+
+// ---------------------------------------------------------------------------
+// Kernel timing hook (slmt_kernel_timing): a pool of event pairs created when
+// recording is switched on, so a recording call itself creates nothing.
+// ---------------------------------------------------------------------------
+namespace {
+constexpr int kTimingSlots = 4096;
+struct KernelTiming {
+  std::mutex mu;
+  bool on = false;
+  std::vector<std::pair<hipEvent_t, hipEvent_t>> pool;
+  int used = 0;
+};
+KernelTiming& kernel_timing() {
+  static KernelTiming t;
+  return t;
+}
+}  // namespace
+
+bool kernel_timing_events(hipEvent_t* start, hipEvent_t* stop) {
+  KernelTiming& t = kernel_timing();
+  std::lock_guard<std::mutex> lock(t.mu);
+  if (!t.on || t.used >= (int)t.pool.size()) return false;
+  *start = t.pool[t.used].first;
+  *stop = t.pool[t.used].second;
+  ++t.used;
+  return true;
+}
+
+int set_kernel_timing(bool enable) {
+  KernelTiming& t = kernel_timing();
+  std::lock_guard<std::mutex> lock(t.mu);
+  if (enable && t.pool.empty()) {
+    t.pool.reserve(kTimingSlots);
+    for (int i = 0; i < kTimingSlots; ++i) {
+      hipEvent_t a, b;
+      if (hipEventCreate(&a) != hipSuccess) return fail(SLMT_ERR_HIP, "timing: hipEventCreate failed");
+      if (hipEventCreate(&b) != hipSuccess) {
+        (void)hipEventDestroy(a);
+        return fail(SLMT_ERR_HIP, "timing: hipEventCreate failed");
+      }
+      t.pool.emplace_back(a, b);
+    }
+  }
+  t.on = enable;
+  return SLMT_OK;
+}
+
+int read_kernel_timing(float* us, int max_n) {
+  KernelTiming& t = kernel_timing();
+  std::lock_guard<std::mutex> lock(t.mu);
+  const int n = std::min(t.used, std::max(max_n, 0));
+  for (int i = 0; i < n; ++i) {
+    float ms = 0.f;
+    if (hipEventSynchronize(t.pool[i].second) != hipSuccess ||
+        hipEventElapsedTime(&ms, t.pool[i].first, t.pool[i].second) != hipSuccess) {
+      t.used = 0;
+      fail(SLMT_ERR_HIP, "timing: reading the decode kernel events failed");
+      return -1;
+    }
+    us[i] = ms * 1000.f;
+  }
+  t.used = 0;
+  return n;
+}
 
 namespace {
 

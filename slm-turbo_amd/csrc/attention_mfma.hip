@@ -34,6 +34,8 @@
 // the dequantized rows.  The per-token min enters once per token as sum(p * min).
 #include "attention_kernel.h"
 
+#include <hip/hip_ext.h>
+
 #include <algorithm>
 #include <cstdlib>
 #include <cstring>
@@ -748,7 +750,11 @@ static int launch(AttnParams p, int groups, hipStream_t stream) {
   p.W = W;
   p.nthreads = S::THREADS;
   p.heads_per_group = 4 * S::WAVES;
-  hipLaunchKernelGGL(kern, dim3(W, groups), dim3(S::THREADS), S::LDS, stream, p);
+  hipEvent_t ev0, ev1;
+  if (kernel_timing_events(&ev0, &ev1))
+    hipExtLaunchKernelGGL(kern, dim3(W, groups), dim3(S::THREADS), S::LDS, stream, ev0, ev1, 0, p);
+  else
+    hipLaunchKernelGGL(kern, dim3(W, groups), dim3(S::THREADS), S::LDS, stream, p);
   if (int rc = check_launch("paged decode")) return rc;
   if (p.B > 0) {
     hipLaunchKernelGGL((merge_kernel<D>), dim3(p.B, (p.H + MH - 1) / MH), dim3(128), 0, stream, p);

@@ -51,6 +51,8 @@
 // a row_newbcast DPP operand.
 #include "attention_kernel.h"
 
+#include <hip/hip_ext.h>
+
 #include <algorithm>
 #include <map>
 #include <mutex>
@@ -802,7 +804,11 @@ static int launch(AttnParams p, int groups, hipStream_t stream) {
   p.W = W;
   p.nthreads = S::THREADS;
   p.heads_per_group = 4 * S::WAVES;
-  hipLaunchKernelGGL(kern, dim3(W, groups), dim3(S::THREADS), S::LDS, stream, p);
+  hipEvent_t ev0, ev1;
+  if (kernel_timing_events(&ev0, &ev1))
+    hipExtLaunchKernelGGL(kern, dim3(W, groups), dim3(S::THREADS), S::LDS, stream, ev0, ev1, 0, p);
+  else
+    hipLaunchKernelGGL(kern, dim3(W, groups), dim3(S::THREADS), S::LDS, stream, p);
   if (int rc = check_launch("paged decode")) return rc;
   if (p.B > 0) {
     hipLaunchKernelGGL((merge_kernel<D, TT>), dim3(p.B, (p.H + MH - 1) / MH), dim3(128), 0, stream, p);

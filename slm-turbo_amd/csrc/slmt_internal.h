@@ -217,6 +217,12 @@ int plan_attention(int B, int H, int G, int D, int dma_kv, AttnPlan* plan);
 bool rows_shape(int H, int G, int D, int cache_kv, int* nkv, int* wpk, int* groups);
 int rows_max_workgroups(int D, int nkv, int wpk, int groups, int cus);
 int launch_attention_rows(int D, int nkv, int wpk, int groups, const AttnParams& p, hipStream_t stream);
+// Event pair for a whole-row decode kernel when slmt_kernel_timing is on: the
+// next free pair of the pool (false when off or full).  The launch passes them
+// to hipExtLaunchKernelGGL, which stamps them from the kernel's own dispatch.
+bool kernel_timing_events(hipEvent_t* start, hipEvent_t* stop);
+int set_kernel_timing(bool enable);            // slmt_kernel_timing
+int read_kernel_timing(float* us, int max_n);  // slmt_kernel_timing_read
 // Matrix-core variant of the whole-row kernel (attention_mfma.hip): whether it
 // serves a whole-row shape (SLMT_PAGED_DECODE=valu turns it off), and its launch.
 bool mfma_rows_enabled(int D, int nkv, int wpk);

@@ -46,6 +46,8 @@ SIGNATURES = {
                                        _i32, _i32, _p_f32, _vp, _i64, _vp]),
     "slmt_prefill_per_channel": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32,
                                         _i32, _i32, _i32, _i32, _i32, _p_f32, _vp, _i64, _vp]),
+    "slmt_kernel_timing": (_i32, [_i32]),
+    "slmt_kernel_timing_read": (_i32, [_p_f32, _i32]),
 }
 
 

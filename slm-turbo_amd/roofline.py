@@ -20,11 +20,11 @@ FP32 vector throughput is 256 flops per CU per clock (4 SIMDs x 16 lanes x
 FMA x packed pairs); ``_estimate_peak_compute`` reports it, which is the
 roof of code that does not use matrix cores (the decode path here).
 
-The 4-bit decode attention path is priced by a second roof as well: the
-VALU *instruction* rate.  Its packed-nibble dot products (v_dot8_u32_u4,
-v_dot2c_f32_f16) retire 16 lanes per SIMD per clock whatever their width,
-so ``valu_lane_ops_per_s`` (= CUs x 64 x clock) and the instruction count
-per token give a time bound independent of bytes (``decode_attention_bounds``).
+The 4-bit decode attention path is priced by two more roofs: the VALU
+*instruction* rate (16 lanes per SIMD per clock whatever an instruction's
+width, ``valu_lane_ops_per_s``) and the matrix-core issue rate (16 cycles per
+16x16x64 int8 or 16x16x32 fp16 product).  ``decode_attention_bounds`` prices
+both decode kernels with their per-token instruction mix.
 """
 from __future__ import annotations
 
@@ -43,6 +43,7 @@ class ArchPeaks:
     fp32_flops_per_cu_clk: int         # vector (non-matrix) FP32
     fp16_mfma_flops_per_cu_clk: int    # dense matrix-core FP16/BF16
     lds_bytes_per_cu: int
+    sustained_clock_ghz: float         # shader clock measured under a full decode load
 
     @property
     def fp32_vector_gflops(self) -> float:
@@ -59,8 +60,8 @@ class ArchPeaks:
 
 
 AMD_ARCHS = {
-    950: ArchPeaks("gfx950", 256, 2.4, 8000.0, 256, 4096, 160 * 1024),
-    942: ArchPeaks("gfx942", 304, 2.1, 5300.0, 256, 2048, 64 * 1024),
+    950: ArchPeaks("gfx950", 256, 2.4, 8000.0, 256, 4096, 160 * 1024, 2.1),
+    942: ArchPeaks("gfx942", 304, 2.1, 5300.0, 256, 2048, 64 * 1024, 2.1),
 }
 
 # NVIDIA: FP32 ops per SM per clock by compute capability, priced at the
@@ -132,34 +133,60 @@ def decode_attention_flops(seq_lens, num_heads: int, head_dim: int) -> int:
     return 4 * head_dim * num_heads * sum(int(x) for x in seq_lens)
 
 
-# VALU lane-operations per (token, query head) of the decode kernel in
-# csrc/attention_kernel.h (one wave = 64 lanes = 16 tokens x 4 heads in QK):
-# * QK: the lane of (token, head) issues 4 * D/8 v_dot8_u32_u4 (4 query
-#   limbs x D/8 key dwords) plus ~6 nibble-sum and score ops;
-# * PV: per token pair a wave issues 8 v_dot2c_f32_f16 + 2 unpack ops on 64
-#   lanes for 2 tokens x 4 heads, i.e. 80 lane-ops per (token, head) at
-#   D = 128 (64 lanes cover 128 dims; scales with D);
-# * softmax, weights: ~30 instructions per 32-token tile: ~15.
-def decode_valu_ops_per_token_head(head_dim: int) -> float:
-    qk = 4 * (head_dim // 8) + 6
-    pv = 80.0 * head_dim / 128
-    return qk + pv + 15.0
+# Per (token, query head) cost of the two whole-row decode kernels, from their
+# compiled main loops and checked against rocprofv3 SQ_INSTS_VALU / SQ_INSTS_MFMA
+# (a wave handles 4 query heads of one KV head, 64 tokens per tile, whatever
+# the group size):
+# * matrix-core kernel (csrc/attention_mfma.hip): per 64-token tile and wave,
+#   VALU = 1.125 D (QK nibble unpack 6 per i8 MFMA, PV operand build 24 per 32
+#   tokens x 32 V bytes) + 289 (limb combine, softmax and weights, addressing),
+#   i.e. 433 wave instructions at D = 128 (measured 433) and 361 at D = 64
+#   (measured 378); matrix cores: 4 D/64 v_mfma_i32_16x16x64_i8 for QK and
+#   8 D/64 v_mfma_f32_16x16x32_f16 for PV, 16 cycles each;
+# * vector-ALU kernel (csrc/attention_rows.hip): QK and PV on v_dot2c_f32_f16
+#   (D/2 lane-ops each per (token, head)), nibble unpack 5 D/32 for QK and D/8
+#   for PV, ~54 for the score, softmax and weights: 218 lane-ops at D = 128
+#   (measured 13.7 wave instructions per (token, KV head)).
+MFMA_CYCLES = 16
+
+
+def decode_valu_ops_per_token_head(head_dim: int, kernel: str = "mfma") -> float:
+    """VALU lane-operations per (token, query head) of the decode kernel."""
+    if kernel == "mfma":
+        return (1.125 * head_dim + 289.0) * 64 / (64 * 4)
+    return 1.28125 * head_dim + 54.0
+
+
+def decode_mfma_cycles_per_token_head(head_dim: int, kernel: str = "mfma") -> float:
+    """Matrix-core cycles (on one SIMD) per (token, query head) of the decode."""
+    if kernel != "mfma":
+        return 0.0
+    per_tile = (4 * head_dim // 64 + 8 * head_dim // 64) * MFMA_CYCLES
+    return per_tile / (64 * 4)
 
 
 def decode_attention_bounds(seq_lens, num_heads: int, num_kv_heads: int, head_dim: int,
-                            device: DeviceProfile, block_size: int = 16) -> dict:
-    """Lower bounds on one decode step's time (seconds) from HBM bandwidth
-    and from the VALU instruction rate, and which one binds."""
+                            device: DeviceProfile, block_size: int = 16, kernel: str = "mfma") -> dict:
+    """Lower bounds on one decode step's time (seconds) from HBM bandwidth,
+    the VALU instruction rate and the matrix-core issue rate, and which one
+    binds.  AMD parts are priced at their sustained clock under this load
+    (2.1 GHz measured on gfx950, below the 2.4 GHz peak clock)."""
     peaks = arch_peaks(device)
     nbytes = decode_attention_bytes(seq_lens, num_heads, num_kv_heads, head_dim, block_size)
     t_hbm = nbytes / (device.memory_bandwidth_gbps * 1e9)
     tokens = sum(int(x) for x in seq_lens)
-    lane_ops = tokens * num_heads * decode_valu_ops_per_token_head(head_dim)
+    lane_ops = tokens * num_heads * decode_valu_ops_per_token_head(head_dim, kernel)
+    mfma_cycles = tokens * num_heads * decode_mfma_cycles_per_token_head(head_dim, kernel)
     if peaks is not None:
-        rate = device.sm_count * 64 * peaks.clock_ghz * 1e9
+        clock = peaks.sustained_clock_ghz * 1e9
+        rate = device.sm_count * 64 * clock
+        t_mfma = mfma_cycles / (device.sm_count * 4) / clock
     else:
         rate = _estimate_peak_compute(device) * 1e9 / 2      # FMA lanes of the reference's table
+        t_mfma = 0.0
     t_valu = lane_ops / rate
+    times = {"hbm": t_hbm, "valu": t_valu, "mfma": t_mfma}
+    bound = max(times, key=times.get)
     return {"bytes": nbytes, "hbm_s": t_hbm, "valu_lane_ops": lane_ops, "valu_s": t_valu,
-            "bound": "hbm" if t_hbm >= t_valu else "valu",
-            "max_hbm_fraction": min(1.0, t_hbm / t_valu) if t_valu > 0 else 1.0}
+            "mfma_cycles": mfma_cycles, "mfma_s": t_mfma, "bound": bound,
+            "max_hbm_fraction": min(1.0, t_hbm / times[bound]) if times[bound] > 0 else 1.0}

@@ -114,16 +114,32 @@ def test_decode_attention_intensity_is_below_the_ridge():
 def test_valu_roof_and_bound_selection():
     dev = rl.mi355x_profile()
     lens = [4096] * 64
-    r = rl.decode_attention_bounds(lens, 32, 8, 128, dev)
-    per = rl.decode_valu_ops_per_token_head(128)
+    # vector-ALU kernel: priced at 218 lane-ops per (token, head) at D = 128 and
+    # the 2.1 GHz sustained clock; at G = 4 it cannot reach the HBM roof
+    r = rl.decode_attention_bounds(lens, 32, 8, 128, dev, kernel="valu")
+    per = rl.decode_valu_ops_per_token_head(128, "valu")
+    assert per == pytest.approx(218.0)
     assert math.isclose(r["valu_lane_ops"], sum(lens) * 32 * per)
-    assert math.isclose(r["valu_s"], r["valu_lane_ops"] / (256 * 64 * 2.4e9))
+    assert math.isclose(r["valu_s"], r["valu_lane_ops"] / (256 * 64 * 2.1e9))
     assert math.isclose(r["hbm_s"], r["bytes"] / 8e12)
-    assert r["bound"] in ("hbm", "valu") and 0 < r["max_hbm_fraction"] <= 1.0
+    assert r["mfma_s"] == 0.0 and r["bound"] == "valu" and r["max_hbm_fraction"] < 0.8
     # doubling the query heads per KV head doubles VALU work, not bytes (much)
-    r8 = rl.decode_attention_bounds(lens, 64, 8, 128, dev)
+    r8 = rl.decode_attention_bounds(lens, 64, 8, 128, dev, kernel="valu")
     assert r8["valu_s"] == pytest.approx(2 * r["valu_s"])
-    assert r8["bound"] == "valu" and r8["max_hbm_fraction"] < r["max_hbm_fraction"]
+    assert r8["max_hbm_fraction"] < r["max_hbm_fraction"]
+
+
+def test_matrix_core_kernel_is_hbm_bound_at_group_4():
+    """The matrix-core decode: 433 VALU wave instructions and 24 16-cycle
+    products per 64-token tile and wave at D = 128 (the counters' figures)."""
+    dev = rl.mi355x_profile()
+    lens = [4096] * 64
+    assert rl.decode_valu_ops_per_token_head(128) * 4 == pytest.approx(433.0)
+    assert rl.decode_mfma_cycles_per_token_head(128) * 64 * 4 == 24 * 16
+    r = rl.decode_attention_bounds(lens, 32, 8, 128, dev)
+    assert r["bound"] == "hbm" and r["max_hbm_fraction"] == 1.0
+    assert r["valu_s"] < r["hbm_s"] and r["mfma_s"] < 0.3 * r["hbm_s"]
+    assert math.isclose(r["mfma_s"], r["mfma_cycles"] / 1024 / 2.1e9)
 
 
 # ---------------------------------------------------------------- device probe
