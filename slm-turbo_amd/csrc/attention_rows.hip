@@ -7,8 +7,9 @@
 // cache row, NKV * (D + 8) bytes) and their 4*WPK query heads each, one wave per 4
 // query heads.  Tiles are TT tokens (64, or 32 where a wave's share of a
 // 64-token tile would cross a paged block).  Work is split stream-K over the
-// concatenated tile list of all sequences, exactly as in attention_kernel.h,
-// and split sequences are merged by the last workgroup to finish a piece.
+// concatenated tile list of all sequences, exactly as in attention_kernel.h;
+// split sequences leave (m, l, o) partials that merge_kernel, launched next on
+// the same stream, combines.
 //
 // Staging: the workgroup copies each tile with 16-byte direct loads
 // (global_load_lds_dwordx4, no VGPRs) into a 2-stage LDS ring, two tiles
