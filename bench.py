@@ -34,7 +34,11 @@ is the headline configuration above):
 * full-model-attention: the attention of one layer of the full-model decode
   step below, batch 32, lengths U[4096, 4224], 32 query / 4 KV heads, head_dim 64.
 
---op-level prints the reference's op-level tables (one JSON line per case):
+--op-level first prints one line per standalone per-channel decode workload
+(batch 1, 4/4 heads, head_dim 64, 512 keys; and 12/2 heads, head_dim 128, 512 /
+1024 / 2048 keys with 1 % outlier channels), each with its roofline object and
+the reference's CPU torch path timed beside it; then the reference's op-level
+tables (one JSON line per case):
 per-channel decode (32/4 and 14/2 heads at head_dim 64, 32/8 at 128; S = 512,
 1024, 2048) and causal prefill (32/4 and 14/2 at 64; S = 512, 1024), each
 against fp16 SDPA over the dequantized K/V broadcast to the query heads.
@@ -51,6 +55,7 @@ from __future__ import annotations
 import argparse
 import ctypes
 import json
+import math
 import os
 import platform
 import statistics
@@ -283,6 +288,80 @@ def cpu_baseline(lens, tables, q, cache_gpu, out_gpu, budget_s: float, w: Worklo
     }
 
 
+def per_channel_configs(kd, dev, timeit, cpu_budget_s) -> None:
+    """The two standalone per-channel decode workloads, one JSON line each, with
+    `roofline` and `cpu_baseline` objects like the paged line's:
+    * batch 1, 4 query / 4 KV heads, head_dim 64, 512 keys, K/V and q ~ N(0,1);
+    * batch 1, 12 query / 2 KV heads (Qwen2-1.5B-shaped), head_dim 128, 512 / 1024 /
+      2048 keys, K/V ~ N(0,1) with 1 % of the channels scaled x8.
+    Bytes per call: packed K and V (KV * S * D), their fp16 scale and zero per
+    channel (8 * KV * D), q fp16 (2 * H * D) and the fp32 output (4 * H * D).
+    `achieved` divides them by the mean time of back-to-back Python calls (these
+    calls are launch-latency bound).  The CPU baseline is the reference's torch
+    composition (oracle/cpu_path.decode_per_channel) on the same inputs."""
+    import torch
+
+    cases = [("per-channel decode, batch 1, 4 q / 4 KV heads, head_dim 64, 512 keys", 4, 4, 64, 512, False)]
+    cases += [(f"per-channel decode, batch 1, 12 q / 2 KV heads, head_dim 128, {S} keys, 1 % outlier channels x8",
+               12, 2, 128, S, True) for S in (512, 1024, 2048)]
+    for name, H, KV, D, S, outliers in cases:
+        g = torch.Generator().manual_seed(S + H)
+        k = torch.randn((KV, S, D), generator=g)
+        v = torch.randn((KV, S, D), generator=g)
+        if outliers:
+            for x in (k, v):
+                n = max(1, math.ceil(0.01 * KV * D))
+                for c in torch.randperm(KV * D, generator=g)[:n].tolist():
+                    x[c // D, :, c % D] *= 8.0
+        q = torch.randn((H, 1, D), generator=g).half().to(dev)
+        kp, ks, kz, vp, vs, vz = kd.quantize_kv(k.half().to(dev), v.half().to(dev))
+        args = (q, kp, ks, kz, vp, vs, vz)
+        run = lambda: kd.kv_dequant_decode_attention(*args, num_kv_heads=KV)
+        out = run()
+        us = timeit(run, 2000, warmup=50)
+        nbytes = KV * S * D + 8 * KV * D + 2 * H * D + 4 * H * D
+        achieved = nbytes / us / 1e3
+        line = {
+            "metric": "per-channel 4-bit decode µs/call + HBM GB/s (% of 8 TB/s)",
+            "value": round(achieved, 3), "unit": "GB/s", "us_per_call": round(us, 2),
+            "higher_is_better": True, "dtype": "int4 codes x fp16 query, fp32 accumulate",
+            "data": "synthetic", "config": {"workload": name, "H": H, "KV": KV, "D": D, "S": S},
+            "roofline": {"bound": "hbm", "achieved": round(achieved, 3), "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 6), "traffic": None,
+                         "algorithmic_bytes": nbytes, "hbm_floor_us": round(nbytes / HBM_PEAK_GBS / 1e3, 4),
+                         "note": "time per back-to-back Python call: launch-latency bound"},
+        }
+        if cpu_budget_s is not None:
+            line["cpu_baseline"] = per_channel_cpu_baseline([t.cpu() for t in args], out.cpu(), nbytes,
+                                                            min(cpu_budget_s, 5.0))
+        print(json.dumps(line), flush=True)
+
+
+def per_channel_cpu_baseline(args, out_gpu, nbytes: int, budget_s: float) -> dict:
+    """oracle/cpu_path.decode_per_channel timed on the host cores."""
+    import torch
+
+    from oracle import cpu_path
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    out = cpu_path.decode_per_channel(*args)
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while time.perf_counter() < t_end and len(times) < 2000:
+        t0 = time.perf_counter()
+        out = cpu_path.decode_per_channel(*args)
+        times.append(time.perf_counter() - t0)
+    t = statistics.median(times)
+    return {
+        "value": round(nbytes / t / 1e9, 4), "unit": "GB/s", "cores": cores, "kind": "port",
+        "sample": f"the whole call, median of {len(times)} runs, {t * 1e6:.1f} µs/run; "
+                  "fp32 SDPA after fp16-rounded dequant",
+        "us_per_call": round(t * 1e6, 1), "cpu_model": cpu_model(),
+        "max_abs_diff_vs_gpu": float((out - out_gpu).abs().max()),
+    }
+
+
 def op_level(args) -> int:
     """The reference's op-level tables (kernels/benchmark/benchmark.py:106-174) on this
     GPU: per-channel decode and causal prefill through the HIP kernels against fp16 SDPA
@@ -316,6 +395,8 @@ def op_level(args) -> int:
     def sdpa(q, k, v, causal):
         with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
             return F.scaled_dot_product_attention(q[None], k[None], v[None], is_causal=causal)[0]
+
+    per_channel_configs(kd, dev, timeit, None if args.no_cpu else args.cpu_seconds)
 
     cases = [("decode", H, KV, D, S, 200) for H, KV, D in ((32, 4, 64), (14, 2, 64), (32, 8, 128))
              for S in (512, 1024, 2048)]
