@@ -45,7 +45,7 @@ enum { SLMT_OUT_F32 = 0, SLMT_OUT_F16 = 1 };
 const char* slmt_last_error(void);
 
 /* ABI version of this library (SLMT_ABI_VERSION). */
-#define SLMT_ABI_VERSION 2
+#define SLMT_ABI_VERSION 3
 int slmt_abi_version(void);
 
 /* Bytes of caller-owned workspace the attention entry points need.  A
@@ -87,6 +87,23 @@ int slmt_quantize_store(const void* key, int64_t key_token_stride,
  */
 int slmt_quantize_per_channel(const void* x, int num_kv_heads, int seq_len, int head_dim,
                               void* packed, void* scale, void* zero, slmt_stream_t stream);
+
+/*
+ * Per-channel append with fixed rulers: the reference's quantize_tensor(x,
+ * scale, zero_point) (host torch code, kernels/benchmark/benchmark.py:45-56),
+ * which its model harness uses to pack new tokens with the rulers frozen at
+ * the first decode (:213-216), on the GPU.
+ *   x:      fp16, element (h, s, d) at x + h*x_head_stride + s*x_seq_stride + d
+ *           (strides in elements, even; x 4-byte aligned)
+ *   scale, zero: fp16 [KV, D] contiguous, 4-byte aligned
+ *   packed: uint8, byte (h, s, j) at packed + h*out_head_stride + s*out_seq_stride + j
+ *           (j < D/2; e.g. a slice of a preallocated [KV, capacity, D/2] cache)
+ * q = clamp(round(x / scale) + zero, 0, 15) with an fp16 result after each op,
+ * bit-exact with the reference's torch arithmetic; dim 2j in the low nibble.
+ */
+int slmt_quantize_with_rulers(const void* x, int64_t x_head_stride, int64_t x_seq_stride, int num_kv_heads,
+                              int seq_len, int head_dim, const void* scale, const void* zero, void* packed,
+                              int64_t out_head_stride, int64_t out_seq_stride, slmt_stream_t stream);
 
 /*
  * Batched paged decode over the packed per-token cache: one launch for the

@@ -191,6 +191,25 @@ int slmt_quantize_per_channel(const void* x, int num_kv_heads, int seq_len, int 
                                      reinterpret_cast<hipStream_t>(stream));
 }
 
+int slmt_quantize_with_rulers(const void* x, int64_t x_head_stride, int64_t x_seq_stride, int num_kv_heads,
+                              int seq_len, int head_dim, const void* scale, const void* zero, void* packed,
+                              int64_t out_head_stride, int64_t out_seq_stride, slmt_stream_t stream) {
+  clear_error();
+  if (!head_dim_ok(head_dim))
+    return fail(SLMT_ERR_INVALID, "quantize_tensor: head_dim must be 64/80/128, got " + s(head_dim));
+  if (num_kv_heads < 0 || seq_len < 0)
+    return fail(SLMT_ERR_INVALID, "quantize_tensor: need KV >= 0 and S >= 0");
+  if (num_kv_heads == 0 || seq_len == 0) return SLMT_OK;
+  if (!x || !scale || !zero || !packed) return fail(SLMT_ERR_INVALID, "quantize_tensor: null pointer argument");
+  if ((x_head_stride & 1) || (x_seq_stride & 1) || !aligned(x, 4) || !aligned(scale, 4) || !aligned(zero, 4))
+    return fail(SLMT_ERR_INVALID, "quantize_tensor: x rows and the rulers must be 4-byte aligned (even strides)");
+  if ((seq_len > 1 && (x_seq_stride < head_dim || out_seq_stride < head_dim / 2)) ||
+      (num_kv_heads > 1 && (x_head_stride < head_dim || out_head_stride < head_dim / 2)))
+    return fail(SLMT_ERR_INVALID, "quantize_tensor: strides smaller than a row");
+  return launch_quantize_rulers(x, x_head_stride, x_seq_stride, num_kv_heads, seq_len, head_dim, scale, zero,
+                                packed, out_head_stride, out_seq_stride, reinterpret_cast<hipStream_t>(stream));
+}
+
 int slmt_decode_paged_batched(const void* q, int64_t q_seq_stride, int64_t q_head_stride,
                               const void* kv_cache, int64_t num_blocks, int block_size,
                               const void* block_tables, int block_table_bits, int64_t block_table_stride,

@@ -99,7 +99,51 @@ quantize_per_channel_kernel(const uint16_t* __restrict__ x, int S, int D,
   }
 }
 
+// Append with fixed rulers (quantize_tensor of the reference,
+// kernels/benchmark/benchmark.py:45-56): the same per-pair arithmetic as the
+// second half of the kernel above, with the scale and zero point given.  One
+// thread per pair of dims (one fp16x2 load, one byte store); the grid's y axis
+// is the KV head.
+__global__ void __launch_bounds__(256)
+quantize_rulers_kernel(const uint16_t* __restrict__ x, int64_t x_head_stride, int64_t x_seq_stride,
+                       int S, int D, const uint16_t* __restrict__ scale, const uint16_t* __restrict__ zero,
+                       uint8_t* __restrict__ packed, int64_t out_head_stride, int64_t out_seq_stride) {
+#pragma clang fp contract(off)
+  const int kv = blockIdx.y;
+  const int half = D / 2;
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= (int64_t)S * half) return;
+  const int s = (int)(t / half);
+  const int j = (int)(t - (int64_t)s * half);
+  const uint32_t w = *reinterpret_cast<const uint32_t*>(x + kv * x_head_stride + s * x_seq_stride + 2 * j);
+  const uint32_t sw = *reinterpret_cast<const uint32_t*>(scale + (int64_t)kv * D + 2 * j);
+  const uint32_t zw = *reinterpret_cast<const uint32_t*>(zero + (int64_t)kv * D + 2 * j);
+  const float x0 = h2f((uint16_t)(w & 0xffffu)), x1 = h2f((uint16_t)(w >> 16));
+  const float sc0 = h2f((uint16_t)(sw & 0xffffu)), sc1 = h2f((uint16_t)(sw >> 16));
+  const float zp0 = h2f((uint16_t)(zw & 0xffffu)), zp1 = h2f((uint16_t)(zw >> 16));
+  // q = clamp(round(x / scale) + zero, 0, 15), an fp16 result after each op
+  const float q0 = clamp_keep_nan(r16(__builtin_rintf(r16(x0 / sc0)) + zp0), 0.0f, 15.0f);
+  const float q1 = clamp_keep_nan(r16(__builtin_rintf(r16(x1 / sc1)) + zp1), 0.0f, 15.0f);
+  const int i0 = (q0 != q0) ? 0 : (int)q0;   // NaN codes -> 0
+  const int i1 = (q1 != q1) ? 0 : (int)q1;
+  packed[kv * out_head_stride + s * out_seq_stride + j] = (uint8_t)(i0 | (i1 << 4));
+}
+
 }  // namespace
+
+int launch_quantize_rulers(const void* x, int64_t x_head_stride, int64_t x_seq_stride, int KV, int S, int D,
+                           const void* scale, const void* zero, void* packed, int64_t out_head_stride,
+                           int64_t out_seq_stride, hipStream_t stream) {
+  if (KV == 0 || S == 0) return SLMT_OK;
+  const int64_t items = (int64_t)S * (D / 2);
+  const int64_t blocks = (items + 255) / 256;
+  if (blocks > 0x7fffffffLL || KV > 65535) return fail(SLMT_ERR_UNSUPPORTED, "quantize_tensor: too large for one launch");
+  hipLaunchKernelGGL(quantize_rulers_kernel, dim3((unsigned)blocks, KV), dim3(256), 0, stream,
+                     reinterpret_cast<const uint16_t*>(x), x_head_stride, x_seq_stride, S, D,
+                     reinterpret_cast<const uint16_t*>(scale), reinterpret_cast<const uint16_t*>(zero),
+                     reinterpret_cast<uint8_t*>(packed), out_head_stride, out_seq_stride);
+  return check_launch("quantize_tensor");
+}
 
 int launch_quantize_per_channel(const void* x, int KV, int S, int D, void* packed,
                                 void* scale, void* zero, hipStream_t stream) {

@@ -148,6 +148,9 @@ int launch_quantize_store(const void* key, int64_t key_stride, const void* value
                           const int64_t* slot_mapping, int64_t N, int KV, int D,
                           hipStream_t stream);
 
+int launch_quantize_rulers(const void* x, int64_t x_head_stride, int64_t x_seq_stride, int KV, int S, int D,
+                           const void* scale, const void* zero, void* packed, int64_t out_head_stride,
+                           int64_t out_seq_stride, hipStream_t stream);
 int launch_quantize_per_channel(const void* x, int KV, int S, int D, void* packed,
                                 void* scale, void* zero, hipStream_t stream);
 

@@ -13,7 +13,7 @@ import os
 import threading
 from pathlib import Path
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 LIB_NAME = "libslmturbo_hip.so"
 LIB_PATH = Path(__file__).resolve().parent / LIB_NAME
 
@@ -34,6 +34,7 @@ SIGNATURES = {
     "slmt_attention_workspace_bytes": (_i64, [_i32, _i32, _i32, _i32]),
     "slmt_quantize_store": (_i32, [_vp, _i64, _vp, _i64, _vp, _i64, _i32, _p_i64, _i64, _i32, _i32, _vp]),
     "slmt_quantize_per_channel": (_i32, [_vp, _i32, _i32, _i32, _vp, _vp, _vp, _vp]),
+    "slmt_quantize_with_rulers": (_i32, [_vp, _i64, _i64, _i32, _i32, _i32, _vp, _vp, _vp, _i64, _i64, _vp]),
     "slmt_decode_paged": (_i32, [_vp, _vp, _i64, _i32, _p_i64, _i32, _i32, _i32, _i32, _p_f32, _vp, _i64,
                                  _vp]),
     "slmt_decode_paged_batched": (_i32, [_vp, _i64, _i64, _vp, _i64, _i32, _vp, _i32, _i64, _p_i32, _i32,

@@ -52,7 +52,13 @@ def _load_native_extension():
     return _native.load()
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def _stream(device: torch.device) -> int:
+    """The current torch stream of ``device`` as a raw hipStream_t."""
+    if _raw_stream is not None:
+        return _raw_stream(torch.cuda.current_device() if device.index is None else device.index)
     return torch.cuda.current_stream(device).cuda_stream
 
 
@@ -70,7 +76,8 @@ _ws_cache: dict = {}
 _need_cache: dict = {}
 
 
-def _workspace(lib, device: torch.device, B: int, H: int, KV: int, D: int) -> tuple[int, int]:
+def _workspace(lib, device: torch.device, B: int, H: int, KV: int, D: int,
+               stream: int | None = None) -> tuple[int, int]:
     nkey = (device.index, B, H, KV, D)
     need = _need_cache.get(nkey)
     if need is None:
@@ -78,7 +85,7 @@ def _workspace(lib, device: torch.device, B: int, H: int, KV: int, D: int) -> tu
         if need < 0:
             raise RuntimeError(_native.last_error(lib))
         _need_cache[nkey] = need
-    key = (device.index, _stream(device))
+    key = (device.index, _stream(device) if stream is None else stream)
     buf = _ws_cache.get(key)
     if buf is None or buf.numel() < need:
         with _ws_lock:
@@ -276,33 +283,40 @@ def kv_quantize_store(key, value, kv_cache, slot_mapping, block_size):
     assert key.dim() == 3, f"key must be [N, KV, D], got {key.shape}"
     assert kv_cache.is_contiguous(), "kv_cache must be contiguous"
     lib = _load_native_extension()
-    _require(key.is_cuda and key.dtype == torch.float16 and value.is_cuda and value.dtype == torch.float16,
-             "store: key/value must be fp16 CUDA")
-    _require(kv_cache.dtype == torch.uint8, "store: kv_cache must be uint8")
-    N, KV, D = key.shape
-    _require(D in _SUPPORTED_D, f"store: head_dim must be 64/80/128, got {D}")
+    # Called once per layer and step: every check reads each attribute once and
+    # formats its message only when it fails.
+    if not (key.is_cuda and value.is_cuda and key.dtype is torch.float16 and value.dtype is torch.float16):
+        raise RuntimeError("store: key/value must be fp16 CUDA")
+    if kv_cache.dtype is not torch.uint8:
+        raise RuntimeError("store: kv_cache must be uint8")
+    kshape = key.shape
+    N, KV, D = kshape
+    if D not in _SUPPORTED_D:
+        raise RuntimeError(f"store: head_dim must be 64/80/128, got {D}")
     SLOT = D + 8
-    _require(kv_cache.size(-1) == SLOT, f"store: cache slot size {kv_cache.size(-1)} != expected {SLOT}")
-    _require(slot_mapping.dtype == torch.int64 and slot_mapping.numel() == N,
-             "store: slot_mapping must be int64 of length N")
-    _require(tuple(value.shape) == (N, KV, D), f"store: value must be [N, KV, D] like key, got {list(value.shape)}")
-    _require(kv_cache.dim() == 4 and kv_cache.size(2) == KV and kv_cache.size(1) == block_size,
-             f"store: kv_cache must be [num_blocks, {block_size}, {KV}, {SLOT}], got {list(kv_cache.shape)}")
+    cshape = kv_cache.shape
+    if cshape[-1] != SLOT:
+        raise RuntimeError(f"store: cache slot size {cshape[-1]} != expected {SLOT}")
+    if slot_mapping.dtype is not torch.int64 or slot_mapping.numel() != N:
+        raise RuntimeError("store: slot_mapping must be int64 of length N")
+    if value.shape != kshape:
+        raise RuntimeError(f"store: value must be [N, KV, D] like key, got {list(value.shape)}")
+    if len(cshape) != 4 or cshape[2] != KV or cshape[1] != block_size:
+        raise RuntimeError(f"store: kv_cache must be [num_blocks, {block_size}, {KV}, {SLOT}], got {list(cshape)}")
     dev = key.device
     with _on_device(dev):
         # token-strided rows are read in place; anything else is made contiguous
-        def rows(t):
-            if t.stride(2) == 1 and t.stride(1) == D and t.stride(0) % 2 == 0:
-                return t, t.stride(0)
-            t = t.contiguous()
-            return t, KV * D
-        key, ks = rows(key)
-        value, vs = rows(value)
+        ks, vs = key.stride(), value.stride()
+        if not (ks[2] == 1 and ks[1] == D and ks[0] % 2 == 0):
+            key, ks = key.contiguous(), (KV * D,)
+        if not (vs[2] == 1 and vs[1] == D and vs[0] % 2 == 0):
+            value, vs = value.contiguous(), (KV * D,)
         slot_mapping = slot_mapping.contiguous()
         rc = lib.slmt_quantize_store(
-            _ptr(key), ks, _ptr(value), vs, _ptr(kv_cache), kv_cache.size(0), int(block_size),
-            _ptr(slot_mapping), N, KV, D, _stream(dev))
-        _native.check(lib, rc)
+            key.data_ptr(), ks[0], value.data_ptr(), vs[0], kv_cache.data_ptr(), cshape[0], int(block_size),
+            slot_mapping.data_ptr(), N, KV, D, _stream(dev))
+        if rc:
+            _native.check(lib, rc)
 
 
 # =============================================================================
@@ -373,37 +387,50 @@ def kv_dequant_decode_paged_batched(
     B, H, D = q.shape
     assert D in (64, 80, 128), f"head_dim must be 64/80/128, got {D}"
     assert H % num_kv_heads == 0, f"H {H} not divisible by num_kv_heads {num_kv_heads}"
-    assert kv_cache.size(-1) == D + 8, f"cache slot must be D+8, got {kv_cache.size(-1)}"
+    cshape = kv_cache.shape
+    assert cshape[-1] == D + 8, f"cache slot must be D+8, got {cshape[-1]}"
     lib = _load_native_extension()
-    _require(q.is_cuda and q.dtype == torch.float16, "paged decode: q must be fp16 CUDA")
-    _require(kv_cache.is_cuda and kv_cache.dtype == torch.uint8 and kv_cache.is_contiguous(),
-             "paged decode: kv_cache must be a contiguous uint8 CUDA tensor")
-    _require(kv_cache.dim() == 4 and kv_cache.size(1) == block_size and kv_cache.size(2) == num_kv_heads,
-             f"paged decode: kv_cache must be [num_blocks, {block_size}, {num_kv_heads}, {D + 8}]")
-    _require(block_tables.dim() == 2 and block_tables.size(0) == B and block_tables.stride(1) == 1
-             and block_tables.dtype in (torch.int32, torch.int64) and block_tables.is_cuda,
-             "paged decode: block_tables must be an int32/int64 CUDA tensor [B, max_blocks]")
-    _require(seq_lens.is_cuda and seq_lens.dtype == torch.int32 and seq_lens.numel() == B,
-             "paged decode: seq_lens must be an int32 CUDA tensor [B]")
+    # Called once per layer and step: every check reads each attribute once and
+    # formats its message only when it fails.
+    if not (q.is_cuda and q.dtype is torch.float16):
+        raise RuntimeError("paged decode: q must be fp16 CUDA")
+    if not (kv_cache.is_cuda and kv_cache.dtype is torch.uint8 and kv_cache.is_contiguous()):
+        raise RuntimeError("paged decode: kv_cache must be a contiguous uint8 CUDA tensor")
+    if not (len(cshape) == 4 and cshape[1] == block_size and cshape[2] == num_kv_heads):
+        raise RuntimeError(f"paged decode: kv_cache must be [num_blocks, {block_size}, {num_kv_heads}, {D + 8}]")
+    bt_dtype = block_tables.dtype
+    bt_stride = block_tables.stride()
+    if not (block_tables.dim() == 2 and block_tables.size(0) == B and bt_stride[1] == 1
+            and (bt_dtype is torch.int32 or bt_dtype is torch.int64) and block_tables.is_cuda):
+        raise RuntimeError("paged decode: block_tables must be an int32/int64 CUDA tensor [B, max_blocks]")
+    if not (seq_lens.is_cuda and seq_lens.dtype is torch.int32 and seq_lens.numel() == B):
+        raise RuntimeError("paged decode: seq_lens must be an int32 CUDA tensor [B]")
     dev = q.device
     with _on_device(dev):
         if out is None:
             out = torch.empty((B, H, D), dtype=out_dtype or torch.float32, device=dev)
-        _require(out.dtype in (torch.float32, torch.float16) and tuple(out.shape) == (B, H, D)
-                 and out.stride(2) == 1, "paged decode: out must be fp32/fp16 [B, H, D] with unit stride over D")
+        out_dtype = out.dtype
+        out_stride = out.stride()
+        if not ((out_dtype is torch.float32 or out_dtype is torch.float16) and out.shape == (B, H, D)
+                and out_stride[2] == 1):
+            raise RuntimeError("paged decode: out must be fp32/fp16 [B, H, D] with unit stride over D")
         if B == 0:
             return out
-        if q.stride(2) != 1 or q.stride(1) % 8 or q.stride(0) % 8 or q.data_ptr() % 16:
+        qs = q.stride()
+        if qs[2] != 1 or qs[1] % 8 or qs[0] % 8 or q.data_ptr() % 16:
             q = q.contiguous()
+            qs = q.stride()
         seq_lens = seq_lens.contiguous()
-        ws, ws_bytes = _workspace(lib, dev, B, H, num_kv_heads, D)
+        stream = _stream(dev)
+        ws, ws_bytes = _workspace(lib, dev, B, H, num_kv_heads, D, stream)
         rc = lib.slmt_decode_paged_batched(
-            _ptr(q), q.stride(0), q.stride(1), _ptr(kv_cache), kv_cache.size(0), int(block_size),
-            _ptr(block_tables), 64 if block_tables.dtype == torch.int64 else 32, block_tables.stride(0),
-            _ptr(seq_lens), 0, B, H, num_kv_heads, D, _ptr(out),
-            _native.OUT_F16 if out.dtype == torch.float16 else _native.OUT_F32,
-            out.stride(0), out.stride(1), ws, ws_bytes, _stream(dev))
-        _native.check(lib, rc)
+            q.data_ptr(), qs[0], qs[1], kv_cache.data_ptr(), cshape[0], int(block_size),
+            block_tables.data_ptr(), 64 if bt_dtype is torch.int64 else 32, bt_stride[0],
+            seq_lens.data_ptr(), 0, B, H, num_kv_heads, D, out.data_ptr(),
+            _native.OUT_F16 if out_dtype is torch.float16 else _native.OUT_F32,
+            out_stride[0], out_stride[1], ws, ws_bytes, stream)
+        if rc:
+            _native.check(lib, rc)
     return out
 
 
@@ -433,6 +460,48 @@ def quantize_per_channel(x):
                                            _stream(dev))
         _native.check(lib, rc)
     return packed, scale, zero
+
+
+def quantize_tensor(x, scale, zero_point, bits=4, out=None):
+    """Quantize + pack with given (fixed) rulers, on the GPU: the reference's
+    quantize_tensor (kernels/benchmark/benchmark.py:45-56), which its model
+    harness uses to append new tokens with the rulers frozen at the first
+    decode (:213-216).
+
+        x:           [KV, S, D] fp16 (unit stride over D)
+        scale, zero_point: [KV, D] fp16, e.g. from quantize_per_channel
+        out:         optional uint8 [KV, S, D//2] (unit stride over the last
+                     dim), e.g. ``cache[:, prev:n]``, written in place
+    Returns the packed codes; bit-exact with the reference's fp16 torch code.
+    """
+    assert bits == 4, "only 4-bit packing is supported"
+    assert x.dim() == 3, f"x must be [KV, S, D], got {tuple(x.shape)}"
+    KV, S, D = x.shape
+    assert D in (64, 80, 128), f"head_dim must be 64/80/128, got {D}"
+    lib = _load_native_extension()
+    if not (x.is_cuda and x.dtype is torch.float16):
+        raise RuntimeError("quantize_tensor: x must be fp16 CUDA")
+    for t in (scale, zero_point):
+        if not (t.is_cuda and t.dtype is torch.float16 and tuple(t.shape) == (KV, D)):
+            raise RuntimeError(f"quantize_tensor: scale/zero_point must be fp16 CUDA [{KV}, {D}]")
+    dev = x.device
+    with _on_device(dev):
+        if out is None:
+            out = torch.empty((KV, S, D // 2), dtype=torch.uint8, device=dev)
+        if not (out.is_cuda and out.dtype is torch.uint8 and tuple(out.shape) == (KV, S, D // 2)
+                and (S == 0 or out.stride(2) == 1)):
+            raise RuntimeError(f"quantize_tensor: out must be uint8 [{KV}, {S}, {D // 2}] with unit stride over the last dim")
+        xs = x.stride()
+        if xs[2] != 1 or xs[1] % 2 or xs[0] % 2 or x.data_ptr() % 4:
+            x = x.contiguous()
+            xs = x.stride()
+        scale, zero_point = scale.contiguous(), zero_point.contiguous()
+        os_ = out.stride()
+        rc = lib.slmt_quantize_with_rulers(x.data_ptr(), xs[0], xs[1], KV, S, D, scale.data_ptr(),
+                                           zero_point.data_ptr(), out.data_ptr(), os_[0], os_[1], _stream(dev))
+        if rc:
+            _native.check(lib, rc)
+    return out
 
 
 def quantize_kv(k, v):

@@ -118,6 +118,21 @@ def test_store_and_quantizer_validation(lib):
     assert b"need KV >= 0 and S >= 1" in lib.slmt_last_error()
 
 
+def test_fixed_ruler_quantizer_validation(lib):
+    q = lib.slmt_quantize_with_rulers
+    assert q(16, 4096, 64, 2, 8, 96, 16, 16, 16, 256, 32, None) == _native.ERR_INVALID
+    assert b"quantize_tensor: head_dim must be 64/80/128" in lib.slmt_last_error()
+    assert q(None, 0, 0, 2, 0, 64, None, None, None, 0, 0, None) == _native.OK      # nothing to do
+    assert q(16, 4096, 64, 2, 8, 64, None, 16, 16, 256, 32, None) == _native.ERR_INVALID
+    assert b"null pointer" in lib.slmt_last_error()
+    assert q(16, 4096, 63, 2, 8, 64, 16, 16, 16, 256, 32, None) == _native.ERR_INVALID
+    assert b"4-byte aligned" in lib.slmt_last_error()
+    assert q(16, 4096, 32, 2, 8, 64, 16, 16, 16, 256, 32, None) == _native.ERR_INVALID
+    assert b"strides smaller than a row" in lib.slmt_last_error()
+    assert q(16, 4096, 64, 2, 8, 64, 16, 16, 16, 256, 16, None) == _native.ERR_INVALID
+    assert b"strides smaller than a row" in lib.slmt_last_error()
+
+
 def test_contiguous_entry_points_validate_block_sizes(lib):
     f = ctypes.c_void_p(16)
     assert lib.slmt_decode_per_token(f, f, f, f, f, f, f, 8, 2, 2, 4, 64, 48, f, None, 0, None) \

@@ -49,6 +49,58 @@ def test_quantize_per_channel_matches_reference_golden(name):
     assert np.array_equal(packed.cpu().numpy(), z[f"{name}__packed"])
 
 
+@pytest.mark.parametrize("name", sorted({k.split("__")[0] for k in np.load(GOLDEN).files}))
+def test_quantize_tensor_with_rulers_matches_reference_golden(name):
+    """The fixed-ruler append packs the reference quantizer's own (x, scale,
+    zero) into exactly the reference's bytes."""
+    z = np.load(GOLDEN)
+    x = torch.from_numpy(z[f"{name}__x"].view(np.float16).copy()).to(DEV)
+    scale = torch.from_numpy(z[f"{name}__scale"].view(np.float16).copy()).to(DEV)
+    zero = torch.from_numpy(z[f"{name}__zero"].view(np.float16).copy()).to(DEV)
+    packed = _kd().quantize_tensor(x, scale, zero)
+    torch.cuda.synchronize()
+    assert np.array_equal(packed.cpu().numpy(), z[f"{name}__packed"])
+
+
+@pytest.mark.parametrize("KV,S0,S1,D", [(2, 64, 1, 128), (4, 512, 37, 64), (2, 100, 300, 80), (1, 16, 8, 128)])
+def test_quantize_tensor_appends_with_frozen_rulers(KV, S0, S1, D):
+    """The reference's model-harness append (kernels/benchmark/benchmark.py:
+    205-216): rulers from the first S0 tokens, new tokens (some outside the
+    rulers' range, so the clamp acts) packed into a slice of a preallocated
+    [KV, capacity, D/2] cache; bytes outside the slice stay as they were."""
+    g = torch.Generator().manual_seed(S0 + S1 + D)
+    x0 = _outliers(torch.randn(KV, S0, D, generator=g), g).half()
+    x1 = (3.0 * torch.randn(KV, S1, D, generator=g)).half()
+    _, scale, zero = _kd().quantize_per_channel(x0.to(DEV))
+    cap = S0 + S1 + 9
+    cache = torch.full((KV, cap, D // 2), 0xA5, dtype=torch.uint8, device=DEV)
+    # a token-strided source, as a slice of a longer [KV, L, D] tensor
+    src = torch.cat([x0, x1], dim=1).to(DEV)[:, S0:, :]
+    _kd().quantize_tensor(src, scale, zero, out=cache[:, S0:S0 + S1])
+    torch.cuda.synchronize()
+    ref = oq.quantize_tensor(x1.numpy(), scale.cpu().numpy(), zero.cpu().numpy())
+    got = cache.cpu().numpy()
+    assert np.array_equal(got[:, S0:S0 + S1], ref)
+    assert (got[:, :S0] == 0xA5).all() and (got[:, S0 + S1:] == 0xA5).all()
+    codes = np.stack([ref & 15, ref >> 4], axis=-1)
+    assert (codes == 0).any() and (codes == 15).any()      # both clamps were exercised
+
+
+def test_quantize_tensor_special_values():
+    """NaN, +-inf, +-0, +-65504 and subnormal inputs against tiny, unit and
+    huge rulers, bit-exact with the oracle (NaN codes become 0 on both)."""
+    D, KV = 64, 2
+    vals = np.array([np.nan, np.inf, -np.inf, 0.0, -0.0, 65504.0, -65504.0, 6e-8, -6e-8, 1.0, -1.0,
+                     0.5, 1.5, 2.5, 7.49, 7.51], dtype=np.float16)
+    x = np.resize(vals, (KV, 8, D)).astype(np.float16)
+    scale = np.resize(np.array([6e-8, 1.0, 4096.0, 0.0133], dtype=np.float16), (KV, D)).astype(np.float16)
+    zero = np.resize(np.array([0.0, 8.0, 15.0, 3.0], dtype=np.float16), (KV, D)).astype(np.float16)
+    got = _kd().quantize_tensor(torch.from_numpy(x).to(DEV), torch.from_numpy(scale).to(DEV),
+                                torch.from_numpy(zero).to(DEV))
+    torch.cuda.synchronize()
+    assert np.array_equal(got.cpu().numpy(), oq.quantize_tensor(x, scale, zero))
+
+
 @pytest.mark.parametrize("KV,S,D", [(4, 512, 64), (2, 2048, 128), (2, 333, 80), (8, 1, 128)])
 def test_quantize_per_channel_matches_oracle(KV, S, D):
     g = torch.Generator().manual_seed(S + D)
