@@ -318,7 +318,7 @@ def per_channel_configs(kd, dev, timeit, cpu_budget_s) -> None:
         args = (q, kp, ks, kz, vp, vs, vz)
         run = lambda: kd.kv_dequant_decode_attention(*args, num_kv_heads=KV)
         out = run()
-        us = timeit(run, 2000, warmup=50)
+        us = timeit(run, 2000, warmup=2000)   # the first calls of a process run while the GPU clocks settle
         nbytes = KV * S * D + 8 * KV * D + 2 * H * D + 4 * H * D
         achieved = nbytes / us / 1e3
         line = {

@@ -6,7 +6,9 @@
 // The reference's op-level decode is one query row over a short context (tens
 // of KB to a few MB of packed K/V), so the call is bound by latency, not by
 // bandwidth: the design minimises the chain of dependent memory round trips
-// and the work on it.  One wave per (KV head kv, chunk of CT keys):
+// and the work on it.  A single wave issues a vector instruction only every
+// ~8 cycles, so the per-wave work must be short: one workgroup of four waves
+// per (KV head kv, chunk of CT keys), each wave CT/4 keys:
 //   * the G query heads of kv, scaled per channel (q'_d = q_d * k_scale_d), go
 //     to LDS;
 //   * QK, 16 keys per round: lane (key t, quarter c) dots its quarter of the
@@ -14,9 +16,11 @@
 //     zero point's term sum_d q'_d k_zero_d is the same for every key of a head,
 //     so it cancels in the softmax and is never formed; the rest is exact fp32
 //     on exact integer codes;
-//   * softmax over the chunk per head (wave reductions), weights to LDS;
-//   * PV: lane = V byte (two dims): sum over the chunk's keys of p * code;
-//   * one chunk: the wave writes the output, o_d = v_scale_d (acc_d / l - v_zero_d).
+//   * softmax over the wave's keys per head (wave reductions), weights to LDS;
+//   * PV: lane = V byte (two dims): sum over the wave's keys of p * code;
+//   * the four waves' (m, l, acc) are combined by log-sum-exp in LDS, wave w
+//     keeping heads w, w + 4;
+//   * one chunk: the waves write the output, o_d = v_scale_d (acc_d / l - v_zero_d).
 //     Several chunks: (m, l, acc) partials go to the workspace with agent-scope
 //     stores and the last chunk of kv to arrive (agent-scope counter) merges
 //     them and resets the counter to zero.
@@ -40,7 +44,8 @@ struct Params {
   int G, S, CT, nchunks, use_quant;
 };
 
-constexpr int MAX_CT = 256;
+constexpr int MAX_CT = 256;     // keys per workgroup
+constexpr int NW = 4;           // waves per workgroup; wave w takes keys [w CT/4, (w+1) CT/4) of the chunk
 
 __device__ __forceinline__ float wave_sum(float x) {
   x += dpp_f<DPP_QUAD_XOR1>(x);
@@ -55,26 +60,34 @@ __device__ __forceinline__ float wave_sum(float x) {
 }
 
 template <int D, int GT>
-__global__ void __launch_bounds__(64) split_kernel(const Params p) {
+__global__ void __launch_bounds__(64 * NW) split_kernel(const Params p) {
   constexpr int QB = D / 8;                 // key bytes per quarter lane
   constexpr int VB = D / 2;                 // V bytes per key
+  constexpr int NB = D == 128 ? 64 : 32;    // lanes holding a head's output (dims 2b, 2b+1)
+  constexpr int HPW = (GT + NW - 1) / NW;   // heads each wave combines and writes
   __shared__ __attribute__((aligned(16))) float qs[GT * D];     // q' of the GT heads (zero past G)
   __shared__ __attribute__((aligned(16))) float sp[MAX_CT * 8];  // scores, then weights: [key][head]
   __shared__ __attribute__((aligned(16))) uint8_t vt[MAX_CT * VB];
+  __shared__ float wml[NW][GT][2];                                // each wave's (m, l) per head
+  __shared__ __attribute__((aligned(16))) float2 wacc[NW][GT][64]; // each wave's PV sums per lane
+  __shared__ float sw[HPW * NW][64];                              // merge coefficients per chunk
   __shared__ int last;
 
-  const int lane = threadIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int chunk = blockIdx.x, kv = blockIdx.y;
   const int tok0 = chunk * p.CT;
   const int ntok = min(p.CT, p.S - tok0);   // >= 1: the host launches ceil(S / CT) chunks
+  const int CTW = p.CT / NW;                // keys per wave, a multiple of 16
+  const int wk0 = wave * CTW;               // this wave's first key within the chunk
+  const int wn = max(0, min(CTW, ntok - wk0));
   const bool quant = p.use_quant != 0;
   const int h0 = kv * p.G;
 
   // round r's codes: lane (key t, quarter c) loads its quarter of key t's K and
-  // V rows (zeros past the chunk); round 0's loads fly while q' is prepared
+  // V rows (zeros past the wave's keys); round 0's loads fly while q' is prepared
   const int t = lane >> 2, c = lane & 3;
-  const uint8_t* kbase = p.kp + ((int64_t)kv * p.S + tok0) * VB + c * QB;
-  const uint8_t* vbase = p.vp + ((int64_t)kv * p.S + tok0) * VB + c * QB;
+  const uint8_t* kbase = p.kp + ((int64_t)kv * p.S + tok0 + wk0) * VB + c * QB;
+  const uint8_t* vbase = p.vp + ((int64_t)kv * p.S + tok0 + wk0) * VB + c * QB;
   struct Codes {
     uint2 k[QB / 8], v[QB / 8];
   };
@@ -83,8 +96,8 @@ __global__ void __launch_bounds__(64) split_kernel(const Params p) {
     const int j = 16 * r + t;
 #pragma unroll
     for (int i = 0; i < QB / 8; ++i) {
-      cd.k[i] = j < ntok ? *reinterpret_cast<const uint2*>(kbase + (int64_t)j * VB + 8 * i) : make_uint2(0u, 0u);
-      cd.v[i] = j < ntok ? *reinterpret_cast<const uint2*>(vbase + (int64_t)j * VB + 8 * i) : make_uint2(0u, 0u);
+      cd.k[i] = j < wn ? *reinterpret_cast<const uint2*>(kbase + (int64_t)j * VB + 8 * i) : make_uint2(0u, 0u);
+      cd.v[i] = j < wn ? *reinterpret_cast<const uint2*>(vbase + (int64_t)j * VB + 8 * i) : make_uint2(0u, 0u);
     }
     return cd;
   };
@@ -92,7 +105,6 @@ __global__ void __launch_bounds__(64) split_kernel(const Params p) {
 
   // q' (straight-line, so every load is in flight at once) and this lane's V
   // rulers for the output dims 2b, 2b+1
-  constexpr int NB = D == 128 ? 64 : 32;
   const int b = lane % NB, par = lane / NB, step = 64 / NB;
   float vsc[2] = {1.f, 1.f}, vzr[2] = {0.f, 0.f};
   if (quant) {
@@ -102,9 +114,7 @@ __global__ void __launch_bounds__(64) split_kernel(const Params p) {
       vzr[e] = h2f(p.vz[(int64_t)kv * D + 2 * b + e]);
     }
   }
-#pragma unroll
-  for (int it = 0; it < GT * D / 64; ++it) {
-    const int i = lane + 64 * it;
+  for (int i = tid; i < GT * D; i += 64 * NW) {
     const int h = i / D, d = i % D;
     float x = 0.f;
     if (h < p.G) {
@@ -116,8 +126,9 @@ __global__ void __launch_bounds__(64) split_kernel(const Params p) {
   __syncthreads();
 
   // ---- QK, 16 keys per round; V rows staged on the way
-  for (int r = 0; r * 16 < ntok; ++r) {
-    const int j = 16 * r + t;               // key within the chunk
+  for (int r = 0; r * 16 < wn; ++r) {
+    const int jw = 16 * r + t;              // key within the wave's keys
+    const int j = wk0 + jw;                 // key within the chunk
     if (r > 0) cur = load_round(r);
     uint32_t kw[QB / 4];
 #pragma unroll
@@ -133,10 +144,10 @@ __global__ void __launch_bounds__(64) split_kernel(const Params p) {
     for (int w = 0; w < QB / 4; ++w) {
       float n[8];
 #pragma unroll
-      for (int b = 0; b < 4; ++b) {
-        const uint32_t byte = (kw[w] >> (8 * b)) & 0xFFu;
-        n[2 * b] = (float)(byte & 15u);
-        n[2 * b + 1] = (float)(byte >> 4);
+      for (int bb = 0; bb < 4; ++bb) {
+        const uint32_t byte = (kw[w] >> (8 * bb)) & 0xFFu;
+        n[2 * bb] = (float)(byte & 15u);
+        n[2 * bb + 1] = (float)(byte >> 4);
       }
       const int d0 = c * (D / 4) + 8 * w;
 #pragma unroll
@@ -160,23 +171,23 @@ __global__ void __launch_bounds__(64) split_kernel(const Params p) {
       float s = dot[h];
       s += dpp_f<DPP_QUAD_XOR1>(s);
       s += dpp_f<DPP_QUAD_XOR2>(s);
-      if ((h & 3) == c && j < ntok) sp[j * 8 + h] = s;
+      if ((h & 3) == c && jw < wn) sp[j * 8 + h] = s;
     }
   }
   __syncthreads();
 
-  // ---- softmax per head over the chunk (base 2)
+  // ---- softmax per head over the wave's keys (base 2)
   const float kscale = 1.4426950408889634f * __builtin_amdgcn_rsqf((float)D);
   float mh[GT], lh[GT];
 #pragma unroll
   for (int h = 0; h < GT; ++h) {
     float mx = -INFINITY;
-    for (int j = lane; j < ntok; j += 64) mx = fmaxf(mx, sp[j * 8 + h] * kscale);
+    for (int j = lane; j < wn; j += 64) mx = fmaxf(mx, sp[(wk0 + j) * 8 + h] * kscale);
     mx = wave_max(mx);
     float ls = 0.f;
-    for (int j = lane; j < ntok; j += 64) {
-      const float e = __builtin_amdgcn_exp2f(sp[j * 8 + h] * kscale - mx);
-      sp[j * 8 + h] = e;
+    for (int j = lane; j < wn; j += 64) {
+      const float e = __builtin_amdgcn_exp2f(sp[(wk0 + j) * 8 + h] * kscale - mx);
+      sp[(wk0 + j) * 8 + h] = e;
       ls += e;
     }
     mh[h] = mx;
@@ -184,11 +195,13 @@ __global__ void __launch_bounds__(64) split_kernel(const Params p) {
   }
   __syncthreads();
 
-  // ---- PV: lane = V byte (dims 2b, 2b+1); head_dim 64: lanes 32-63 take the odd keys
+  // ---- PV over the wave's keys: lane = V byte (dims 2b, 2b+1); head_dim 64:
+  // lanes 32-63 take the odd keys
   float acc[GT][2];
 #pragma unroll
   for (int h = 0; h < GT; ++h) acc[h][0] = acc[h][1] = 0.f;
-  for (int j = par; j < ntok; j += step) {
+  for (int jw = par; jw < wn; jw += step) {
+    const int j = wk0 + jw;
     const uint32_t byte = vt[j * VB + b];
     const float nlo = (float)(byte & 15u), nhi = (float)(byte >> 4);
     float w[8];
@@ -211,6 +224,42 @@ __global__ void __launch_bounds__(64) split_kernel(const Params p) {
     }
   }
 
+  // ---- the chunk's four waves combined (log-sum-exp) in LDS; wave w then
+  // owns heads w, w + NW, ...
+#pragma unroll
+  for (int h = 0; h < GT; ++h) {
+    wacc[wave][h][lane] = make_float2(acc[h][0], acc[h][1]);
+    if (lane == 0) {
+      wml[wave][h][0] = mh[h];
+      wml[wave][h][1] = lh[h];
+    }
+  }
+  __syncthreads();
+  float cm[HPW], cl[HPW];
+  float2 ca[HPW];
+#pragma unroll
+  for (int k = 0; k < HPW; ++k) {
+    const int h = wave + NW * k;
+    cm[k] = -INFINITY;
+    cl[k] = 0.f;
+    ca[k] = make_float2(0.f, 0.f);
+    if (h < GT) {
+      float M = -INFINITY;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) M = fmaxf(M, wml[w][h][0]);
+#pragma unroll
+      for (int w = 0; w < NW; ++w) {
+        const float mw = wml[w][h][0];
+        const float f = mw == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mw - M);   // waves without keys: 0
+        cl[k] += f * wml[w][h][1];
+        const float2 a = wacc[w][h][lane];
+        ca[k].x += f * a.x;
+        ca[k].y += f * a.y;
+      }
+      cm[k] = M;
+    }
+  }
+
   auto write_out = [&](int h, float o0, float o1) {   // o: sum p * code / l, dims 2b, 2b+1
     const int d = 2 * b;
     if (quant) {
@@ -223,58 +272,74 @@ __global__ void __launch_bounds__(64) split_kernel(const Params p) {
   if (p.nchunks == 1) {
     if (lane < NB) {
 #pragma unroll
-      for (int h = 0; h < GT; ++h)
-        if (h < p.G) write_out(h, acc[h][0] / lh[h], acc[h][1] / lh[h]);
+      for (int k = 0; k < HPW; ++k) {
+        const int h = wave + NW * k;
+        if (h < GT && h < p.G) write_out(h, ca[k].x / cl[k], ca[k].y / cl[k]);
+      }
     }
     return;
   }
 
   // ---- partials, arrival, and the last arriver's merge
   float* mypart = p.part + ((int64_t)kv * p.nchunks + chunk) * GT * (D + 2);
-  if (lane < NB) {
 #pragma unroll
-    for (int h = 0; h < GT; ++h) store_pair_agent(mypart + h * (D + 2) + 2 * b, acc[h][0], acc[h][1]);
-  }
-  if (lane == 0) {
-#pragma unroll
-    for (int h = 0; h < GT; ++h) store_pair_agent(mypart + h * (D + 2) + D, mh[h], lh[h]);
+  for (int k = 0; k < HPW; ++k) {
+    const int h = wave + NW * k;
+    if (h < GT) {
+      if (lane < NB) store_pair_agent(mypart + h * (D + 2) + 2 * b, ca[k].x, ca[k].y);
+      if (lane == 0) store_pair_agent(mypart + h * (D + 2) + D, cm[k], cl[k]);
+    }
   }
   vm_drain();
   __syncthreads();
-  if (lane == 0) {
+  if (tid == 0) {
     const int prev = __hip_atomic_fetch_add(p.counters + kv, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     last = prev == p.nchunks - 1;
   }
   __syncthreads();
   if (!last) return;
-  // (m, l) of every chunk at once: lane k loads chunk k's for all heads; the
-  // merge coefficients exp2(m_k - M) / L go to LDS
+  // (m, l) of every chunk at once: lane k loads chunk k's for the wave's heads;
+  // the merge coefficients exp2(m_k - M) / L go to LDS
   const float* kvpart = p.part + (int64_t)kv * p.nchunks * GT * (D + 2);
-  float mk[GT], lk[GT];
 #pragma unroll
-  for (int h = 0; h < GT; ++h) {
-    mk[h] = -INFINITY;
-    lk[h] = 0.f;
-  }
-  if (lane < p.nchunks) {
-#pragma unroll
-    for (int h = 0; h < GT; ++h) {
+  for (int k = 0; k < HPW; ++k) {
+    const int h = wave + NW * k;
+    if (h >= GT) continue;
+    float mk = -INFINITY, lk = 0.f;
+    if (lane < p.nchunks) {
       const float2 ml = load_pair_agent(kvpart + ((int64_t)lane * GT + h) * (D + 2) + D);
-      mk[h] = ml.x;
-      lk[h] = ml.y;
+      mk = ml.x;
+      lk = ml.y;
     }
-  }
-#pragma unroll
-  for (int h = 0; h < GT; ++h) {
-    const float M = wave_max(mk[h]);
-    const float w = lane < p.nchunks ? __builtin_amdgcn_exp2f(mk[h] - M) : 0.f;
-    const float L = wave_sum(w * lk[h]);
-    sp[h * 64 + lane] = w / L;
+    const float M = wave_max(mk);
+    const float w = lane < p.nchunks ? __builtin_amdgcn_exp2f(mk - M) : 0.f;
+    const float L = wave_sum(w * lk);
+    sw[k * NW + wave][lane] = w / L;
   }
   __syncthreads();
   // outputs: lane b owns dims 2b, 2b+1 (head_dim 64: lanes 32-63 take the odd
   // chunks); the partial outputs are loaded 8 at a time before they are used
-  auto finish_head = [&](int h, float o0, float o1) {
+#pragma unroll
+  for (int k = 0; k < HPW; ++k) {
+    const int h = wave + NW * k;
+    if (h >= GT || h >= p.G) continue;
+    const float* cf = sw[k * NW + wave];
+    float o0 = 0.f, o1 = 0.f;
+    for (int k0 = par; k0 < p.nchunks; k0 += 8 * step) {
+      float2 ov[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int kk = k0 + i * step;
+        ov[i] = kk < p.nchunks ? load_pair_agent(kvpart + ((int64_t)kk * GT + h) * (D + 2) + 2 * b) : make_float2(0.f, 0.f);
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int kk = k0 + i * step;
+        const float f = kk < p.nchunks ? cf[kk] : 0.f;
+        o0 = __builtin_fmaf(f, ov[i].x, o0);
+        o1 = __builtin_fmaf(f, ov[i].y, o1);
+      }
+    }
     if (D == 64) {
       float a0, a1;
       swap32(o0, a0, a1);
@@ -282,58 +347,14 @@ __global__ void __launch_bounds__(64) split_kernel(const Params p) {
       swap32(o1, a0, a1);
       o1 = a0 + a1;
     }
-    if (lane < NB && h < p.G) write_out(h, o0, o1);
-  };
-  if (p.nchunks <= 16) {
-    // straight-line: every head's loads can be in flight together
-#pragma unroll
-    for (int h = 0; h < GT; ++h) {
-      float2 ov[16 / (64 / NB)];
-#pragma unroll
-      for (int i = 0; i < 16 / step; ++i) {
-        const int k = par + i * step;
-        ov[i] = k < p.nchunks ? load_pair_agent(kvpart + ((int64_t)k * GT + h) * (D + 2) + 2 * b) : make_float2(0.f, 0.f);
-      }
-      float o0 = 0.f, o1 = 0.f;
-#pragma unroll
-      for (int i = 0; i < 16 / step; ++i) {
-        const int k = par + i * step;
-        const float cf = k < p.nchunks ? sp[h * 64 + k] : 0.f;
-        o0 = __builtin_fmaf(cf, ov[i].x, o0);
-        o1 = __builtin_fmaf(cf, ov[i].y, o1);
-      }
-      finish_head(h, o0, o1);
-    }
-    if (lane == 0) __hip_atomic_store(p.counters + kv, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    return;
+    if (lane < NB) write_out(h, o0, o1);
   }
-#pragma unroll
-  for (int h = 0; h < GT; ++h) {
-    if (h >= p.G) break;
-    float o0 = 0.f, o1 = 0.f;
-    for (int k0 = par; k0 < p.nchunks; k0 += 8 * step) {
-      float2 ov[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int k = k0 + i * step;
-        ov[i] = k < p.nchunks ? load_pair_agent(kvpart + ((int64_t)k * GT + h) * (D + 2) + 2 * b) : make_float2(0.f, 0.f);
-      }
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int k = k0 + i * step;
-        const float cf = k < p.nchunks ? sp[h * 64 + k] : 0.f;
-        o0 = __builtin_fmaf(cf, ov[i].x, o0);
-        o1 = __builtin_fmaf(cf, ov[i].y, o1);
-      }
-    }
-    finish_head(h, o0, o1);
-  }
-  if (lane == 0) __hip_atomic_store(p.counters + kv, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (tid == 0) __hip_atomic_store(p.counters + kv, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 template <int D, int GT>
 int launch(const Params& p, int KV, hipStream_t stream) {
-  hipLaunchKernelGGL((split_kernel<D, GT>), dim3(p.nchunks, KV), dim3(64), 0, stream, p);
+  hipLaunchKernelGGL((split_kernel<D, GT>), dim3(p.nchunks, KV), dim3(64 * NW), 0, stream, p);
   return check_launch("per-channel decode");
 }
 
@@ -345,13 +366,14 @@ int launch_decode_channel_split(const void* q, const void* kp, const void* ks, c
   (void)kz;   // the key zero point cancels in the softmax
   if ((D != 64 && D != 128) || G < 1 || G > 8 || S < 1) return SLMT_ERR_UNSUPPORTED;
   const int KV = H / G;
-  // chunk size: the smallest power of two from 16 that gives at most 16 chunks
-  // per KV head (the merge reads every chunk's partials) and at most 512
-  // workgroups; past 4096 keys the chunks stay at 256 keys, up to 64 of them
-  int ct = 16;
+  // chunk size: workgroups of four waves, each wave a multiple of 16 keys; the
+  // smallest power of two from 64 keys per workgroup that gives at most 32
+  // chunks per KV head (the merge reads every chunk's partials) and at most
+  // 256 workgroups; past 16384 keys the general kernel takes over (64 chunks)
+  int ct = 64;
   while (ct < chan::MAX_CT) {
     const int n = (S + ct - 1) / ct;
-    if (n <= 16 && n * KV <= 512) break;
+    if (n <= 32 && n * KV <= 256) break;
     ct *= 2;
   }
   const int nchunks = (S + ct - 1) / ct;

@@ -16,12 +16,22 @@ from oracle import quant as oq
 ATOL, RTOL = 2e-3, 1e-2
 
 
+# Every assert_close records (what, max abs error, share of the bar used) here;
+# tests/conftest.py writes the list out when SLMT_ENVELOPE_OUT names a file.
+ENVELOPE: list = []
+
+
 def assert_close(got, ref, atol=ATOL, rtol=RTOL, what="output"):
     got = np.asarray(got, dtype=np.float64)
     ref = np.asarray(ref, dtype=np.float64)
     assert got.shape == ref.shape, (got.shape, ref.shape)
     both_nan = np.isnan(got) & np.isnan(ref)
     err = np.abs(got - ref)
+    if got.size:
+        e = np.where(both_nan, 0.0, err)
+        ENVELOPE.append({"what": what, "max_abs_err": float(np.nanmax(e)),
+                         "bar_used": float(np.nanmax(e / (atol + rtol * np.abs(np.nan_to_num(ref))))),
+                         "atol": atol, "rtol": rtol})
     bad = ~both_nan & ~(err <= atol + rtol * np.abs(ref))
     if bad.any():
         i = np.unravel_index(np.argmax(np.where(bad, err, -1)), got.shape)

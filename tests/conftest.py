@@ -18,6 +18,22 @@ def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (HIP) GPU; skipped without one")
 
 
+def pytest_sessionfinish(session, exitstatus):
+    """With SLMT_ENVELOPE_OUT set, write every parity check's largest error and
+    the share of the tolerance it used (the measured precision envelope)."""
+    import os
+
+    path = os.environ.get("SLMT_ENVELOPE_OUT")
+    if not path:
+        return
+    import json
+
+    from common import ENVELOPE
+
+    Path(path).parent.mkdir(parents=True, exist_ok=True)
+    Path(path).write_text(json.dumps(ENVELOPE, indent=0))
+
+
 def pytest_collection_modifyitems(config, items):
     import torch
 
