@@ -23,7 +23,9 @@
 // * V enters as n - zr, zr the zero point rounded and clamped to 0..15 (the
 //   reference quantizer's zero points are such integers), and the finished row
 //   is o_d = s_d * (sum p (n - zr) / l - (z_d - zr_d)) in fp32.
-// * P enters in fp16 (relative 2^-11 per weight), as the decode's weights do.
+// * P enters in fp16 (relative 2^-11 per weight), as the decode's weights do, and
+//   the row sums l are a product of the same fp16 weights with a block of ones,
+//   so numerator and denominator see the same rounded weights.
 // use_quant = 0 takes the raw codes (scale 1, zero 0).  Causal row m sees keys
 // n <= m; keys past S are masked.  S = 0 yields NaN rows (0/0), as the
 // reference's kernels do.
@@ -139,8 +141,21 @@ __global__ void __launch_bounds__(256) prefill_kernel(const Params p) {
   // before it is computed, and written to LDS one tile before.
   uint2 kx[2][GG::KW];
   uint32_t vx[2][GG::VW][2];
+  const uint8_t* const ksrc0 = kbase + (int64_t)kk * (D / 2) + ku * (D / 8);
+  const uint8_t* const vsrc0 = vbase + (int64_t)(2 * vk) * (D / 2) + 4 * vb;
   auto load = [&](int t, auto slot) {   // the tile's codes (keys past S re-read key S - 1)
     constexpr int sl = decltype(slot)::value;
+    if ((t + 1) * BN <= p.S) {             // uniform: every key of the tile lies before S
+      const int64_t off = (int64_t)t * BN * (D / 2);
+#pragma unroll
+      for (int i = 0; i < GG::KW; ++i) kx[sl][i] = *reinterpret_cast<const uint2*>(ksrc0 + off + 8 * i);
+#pragma unroll
+      for (int r = 0; r < GG::VW; ++r) {
+        vx[sl][r][0] = *reinterpret_cast<const uint32_t*>(vsrc0 + off + 32 * r);
+        vx[sl][r][1] = *reinterpret_cast<const uint32_t*>(vsrc0 + off + D / 2 + 32 * r);
+      }
+      return;
+    }
     const int key = min(t * BN + kk, p.S - 1);
     const uint8_t* ksrc = kbase + (int64_t)key * (D / 2) + ku * (D / 8);
 #pragma unroll
@@ -192,7 +207,12 @@ __global__ void __launch_bounds__(256) prefill_kernel(const Params p) {
   floatx4 o[D / 16];
 #pragma unroll
   for (int c = 0; c < D / 16; ++c) o[c] = floatx4{0.f, 0.f, 0.f, 0.f};
-  float m_run = -INFINITY, l_run = 0.f;
+  // the row sums l come out of the matrix cores as a product with a block of
+  // ones, from the same fp16 weights the output uses
+  floatx4 ol = floatx4{0.f, 0.f, 0.f, 0.f};
+  const half8 ones = half8{(_Float16)1.0f, (_Float16)1.0f, (_Float16)1.0f, (_Float16)1.0f,
+                           (_Float16)1.0f, (_Float16)1.0f, (_Float16)1.0f, (_Float16)1.0f};
+  float m_run = -INFINITY;
 
   using S0 = std::integral_constant<int, 0>;
   using S1 = std::integral_constant<int, 1>;
@@ -246,27 +266,24 @@ __global__ void __launch_bounds__(256) prefill_kernel(const Params p) {
     }
     tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
     tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-    const float m_new = fmaxf(m_run, tmax);                  // finite: key 0 is visible to every row
-    // rescale the running sums only when some column's maximum grew (alpha = 0
-    // from the initial -inf, 1 where it did not grow)
-    if (__builtin_amdgcn_ballot_w64(m_new > m_run)) {
+    // The reference maximum moves only when some column's maximum exceeds it by
+    // more than 2^8 (base-2 logits): the weights then stay below 256, well inside
+    // fp16, and the running sums are rescaled rarely (alpha = 0 from the initial
+    // -inf, 1 where a column's maximum did not grow).  Key 0 is visible to every
+    // row, so the first tile sets a finite maximum.
+    if (__builtin_amdgcn_ballot_w64(tmax > m_run + 8.0f)) {
+      const float m_new = fmaxf(m_run, tmax);
       const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-      l_run *= alpha;
+      ol *= alpha;
 #pragma unroll
       for (int c = 0; c < D / 16; ++c) o[c] *= alpha;
+      m_run = m_new;
     }
     half4 pb[4];
-    float ls = 0.f;
 #pragma unroll
     for (int n = 0; n < 4; ++n)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float pv = __builtin_amdgcn_exp2f(s[n][i] - m_new);
-        ls += pv;
-        pb[n][i] = (_Float16)pv;
-      }
-    l_run += ls;
-    m_run = m_new;
+      for (int i = 0; i < 4; ++i) pb[n][i] = (_Float16)__builtin_amdgcn_exp2f(s[n][i] - m_run);
     // O^T: dims 16 c + 4 grp + i.  One product covers 32 keys: the lane's 8
     // k slots are keys 32 hh + 4 grp + i and 32 hh + 16 + 4 grp + i (i < 4), the
     // same keys in the V^T operand (A) and in the weights (B = pb[2 hh], pb[2 hh + 1])
@@ -281,6 +298,11 @@ __global__ void __launch_bounds__(256) prefill_kernel(const Params p) {
         const half8 b = __builtin_shufflevector(pb[2 * hh], pb[2 * hh + 1], 0, 1, 2, 3, 4, 5, 6, 7);
         o[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, o[c], 0, 0, 0);
       }
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      const half8 b = __builtin_shufflevector(pb[2 * hh], pb[2 * hh + 1], 0, 1, 2, 3, 4, 5, 6, 7);
+      ol = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, b, ol, 0, 0, 0);
+    }
     if (t + 1 < ntiles) store(Next{});
     __syncthreads();
   };
@@ -289,10 +311,8 @@ __global__ void __launch_bounds__(256) prefill_kernel(const Params p) {
     if (t + 1 < ntiles) iteration(t + 1, S1{});
   }
 
-  // the 4 lane groups of a column hold disjoint keys: add their sums
-  float lt = l_run + __shfl_xor(l_run, 16, 64);
-  lt += __shfl_xor(lt, 32, 64);
-  const float rl = 1.0f / lt;
+  // every row of the ones product holds the column's whole sum
+  const float rl = 1.0f / ol[0];
   if (m < p.M) {
     float* orow = p.out + ((int64_t)h * p.M + m) * D;
 #pragma unroll
