@@ -4,8 +4,8 @@
 //
 // Prefill is GEMM-shaped (every key meets up to 64 query rows of a tile), so
 // unlike the decode it runs on the matrix cores.  A workgroup takes 64 query rows
-// of one query head, one wave per 16 rows, and walks the 64-key tiles the rows
-// can see.  Everything is kept transposed, so a lane owns one query column from
+// of one query head (of two, for long prefills), one wave per 16 rows of a head,
+// and walks the 64-key tiles the rows can see.  Everything is kept transposed, so a lane owns one query column from
 // the scores to the output:
 //   S^T = K Q'^T     (v_mfma_f32_16x16x32_f16: A = K rows, B = the lane's query)
 //   P^T = exp2(S^T - m)      (online softmax per query column)
@@ -30,6 +30,9 @@
 // n <= m; keys past S are masked.  S = 0 yields NaN rows (0/0), as the
 // reference's kernels do.
 //
+// A workgroup takes 64 query rows of one query head (4 waves), or of two query
+// heads of the same KV head (8 waves) for long prefills; the first four waves
+// stage the tiles for all of them.
 // Staging: the workgroup converts each tile into a 2-stage LDS ring: K as
 // [key][dim] fp16 rows padded to D*2+16 bytes (16-byte operand reads of 8 rows at
 // once hit 8 disjoint bank groups), V^T as [dim][key] fp16 rows padded to 136
@@ -80,13 +83,17 @@ __device__ __forceinline__ uint32_t nib_pair(uint32_t lo_all, uint32_t hi_all, i
   return __builtin_bit_cast(uint32_t, r);
 }
 
-template <int D>
-__global__ void __launch_bounds__(256) prefill_kernel(const Params p) {
+// HP query heads of one KV head per workgroup (4 waves each, the same 64 query
+// rows): the K/V tiles are staged once, by the first four waves, for all of them.
+template <int D, int HP>
+__global__ void __launch_bounds__(256 * HP) prefill_kernel(const Params p) {
   using GG = Geo<D>;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int h = blockIdx.x % p.H;
-  const int qb = p.qblocks - 1 - (int)(blockIdx.x / p.H);   // the longest query blocks first
+  const int tid = threadIdx.x, lane = tid & 63, w = (tid >> 6) & 3;
+  const bool stager = tid < 256;                              // uniform per wave
+  const int hgroups = p.H / HP;
+  const int h = (blockIdx.x % hgroups) * HP + (tid >> 8);
+  const int qb = p.qblocks - 1 - (int)(blockIdx.x / hgroups);   // the longest query blocks first
   const int kv = h / p.G;
   const int m0 = qb * BM;
   const int col = lane & 15, grp = lane >> 4;
@@ -145,6 +152,7 @@ __global__ void __launch_bounds__(256) prefill_kernel(const Params p) {
   const uint8_t* const vsrc0 = vbase + (int64_t)(2 * vk) * (D / 2) + 4 * vb;
   auto load = [&](int t, auto slot) {   // the tile's codes (keys past S re-read key S - 1)
     constexpr int sl = decltype(slot)::value;
+    if (!stager) return;
     if ((t + 1) * BN <= p.S) {             // uniform: every key of the tile lies before S
       const int64_t off = (int64_t)t * BN * (D / 2);
 #pragma unroll
@@ -169,6 +177,7 @@ __global__ void __launch_bounds__(256) prefill_kernel(const Params p) {
   };
   auto store = [&](auto slot) {  // slot's codes -> fp16 (code - zero) in LDS stage `slot`
     constexpr int sl = decltype(slot)::value;
+    if (!stager) return;
     uint8_t* Ks = smem + sl * GG::STAGE;
     uint8_t* Vs = Ks + GG::KBYTES;
     uint32_t kw[D / 8];
@@ -330,16 +339,26 @@ __global__ void __launch_bounds__(256) prefill_kernel(const Params p) {
   }
 }
 
-template <int D>
-int launch(const Params& p, hipStream_t stream) {
+template <int D, int HP>
+int launch_hp(const Params& p, hipStream_t stream) {
   static const bool lds_ok = [] {   // above 64 KB of LDS (head_dim 128) needs the attribute
-    return hipFuncSetAttribute(reinterpret_cast<const void*>(prefill_kernel<D>),
+    return hipFuncSetAttribute(reinterpret_cast<const void*>(prefill_kernel<D, HP>),
                                hipFuncAttributeMaxDynamicSharedMemorySize, Geo<D>::LDS) == hipSuccess;
   }();
   if (!lds_ok) return fail(SLMT_ERR_HIP, "prefill: could not grant the kernel its LDS");
-  const int grid = p.qblocks * p.H;
-  hipLaunchKernelGGL(prefill_kernel<D>, dim3(grid), dim3(256), Geo<D>::LDS, stream, p);
+  const int grid = p.qblocks * (p.H / HP);
+  hipLaunchKernelGGL((prefill_kernel<D, HP>), dim3(grid), dim3(256 * HP), Geo<D>::LDS, stream, p);
   return check_launch("prefill");
+}
+
+// Two query heads per workgroup where a KV head has an even number of them and
+// the grid stays above 256 such workgroups (long prefills): the staging work per
+// query row halves.  Short prefills keep one head per workgroup and twice the
+// workgroups.
+template <int D>
+int launch(const Params& p, hipStream_t stream) {
+  if (p.G % 2 == 0 && (int64_t)p.qblocks * (p.H / 2) > 256) return launch_hp<D, 2>(p, stream);
+  return launch_hp<D, 1>(p, stream);
 }
 
 }  // namespace prefill
