@@ -15,6 +15,13 @@
 // query heads (WPK waves per KV head); 64-token tiles are copied with 16-byte
 // direct loads into a 2-stage LDS ring two tiles ahead; work is split stream-K
 // over the concatenated tile list and split sequences are merged by merge_kernel.
+// At head_dim 128 with 8 query heads per KV head the two waves of a KV head
+// split each tile's tokens instead (32 each, all 8 heads as two sets of B
+// columns), so the nibble unpacking of K and V is done once per token rather
+// than once per wave; the second wave's sums join the first's through LDS at
+// each segment end.  At head_dim 64 the split measured slower (the extra
+// softmax reductions and the join cost more than the unpacking saved) and the
+// two waves take 4 heads each over the whole tile.
 //
 // QK, exact: v_mfma_i32_16x16x64_i8.  The fp16 query of each head is scaled by a
 // power of two to a 31-bit integer Q (every fp16 value above 2^-21 of the head's
@@ -82,7 +89,13 @@ struct Shape {
   static constexpr int MOFF = ZOFF + 128;
   static constexpr int STASH = 256;             // sequence lengths kept in LDS
   static constexpr int SOFF = MOFF + 32 * 4;
-  static constexpr int LDS = SOFF + STASH * 4;
+  // Two waves per KV head split each tile's tokens and take all of the KV head's
+  // 8 query heads; at a segment end the second wave hands its (m, l, PV sums)
+  // to the first through this buffer: per KV head 64 lanes x D/4 floats + 3 x 8.
+  static constexpr int CBW = (D / 4) * 64 * 4 + 3 * 8 * 4;
+  static constexpr int COFF = SOFF + STASH * 4;
+  static constexpr bool TS = WPK == 2 && D == 128;   // token split (see mfma_kernel)
+  static constexpr int LDS = COFF + (TS ? NKV * CBW : 0);
   static_assert(LDS <= 160 * 1024, "LDS ring too large");
 };
 
@@ -107,6 +120,16 @@ template <int D, int NKV, int WPK>
 __global__ void __launch_bounds__(NKV * WPK * 64) mfma_kernel(const AttnParams p) {
   using S = Shape<D, NKV, WPK>;
   constexpr int TT = S::TT, SLOT = S::SLOT, RB = S::RB, KB = S::KB, CB = S::CB, TH = S::TH;
+  // Token split (two waves per KV head): wave `half` of a KV head takes tokens
+  // 32 half .. 32 half + 31 of every tile for all 8 query heads of the KV head
+  // (two sets of 4), so the K unpacking and the V operands are built once per
+  // token instead of once per wave.
+  constexpr bool TS = S::TS;
+  constexpr int NSET = TS ? 2 : 1;         // sets of 4 query heads per wave
+  constexpr int RBW = TS ? RB / 2 : RB;    // QK row blocks per wave
+  constexpr int THW = TS ? 1 : TH;         // PV token halves per wave
+  constexpr int TTW = TT / (TS ? 2 : 1);   // tokens per wave and tile
+  constexpr int HPW = 4 * NSET;            // query heads per wave
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
 
   const int tid = threadIdx.x;
@@ -118,6 +141,7 @@ __global__ void __launch_bounds__(NKV * WPK * 64) mfma_kernel(const AttnParams p
   const int kv_lo = group * NKV;
   const int kvw = wave / WPK;                                     // the wave's KV head within the group
   const int hw = h0 + 4 * wave;                                   // the wave's first query head
+  const int half = TS ? (wave & 1) : 0;                           // token half (token split)
   int* misc = reinterpret_cast<int*>(smem + S::MOFF);
   uint8_t* const wscr = smem + S::WOFF + wave * S::WSZ;
   if (tid < 32) reinterpret_cast<uint32_t*>(smem + S::ZOFF)[tid] = 0u;   // published by schedule_range's barriers
@@ -253,27 +277,32 @@ __global__ void __launch_bounds__(NKV * WPK * 64) mfma_kernel(const AttnParams p
   auto kbase = [&](int kb) { return D == 128 ? 32 * grp + 16 * kb : 16 * grp; };
   const uint8_t* const qsl = smem + S::QOFF + wave * 1024;
 
-  v4i qb[KB];                          // B operand: limb lx of head hq's scaled query, k-set grp
-  float qa = 0.f, qs = 0.f, mq = 0.f, m_run = -INFINITY, l_run = 0.f, vmt = 0.f;
+  v4i qb[NSET][KB];                    // B operand: limb lx of head set st's head hq, k-set grp
+  float qa[NSET], qs[NSET], mq[NSET], m_run[NSET], l_run[NSET], vmt[NSET];
+#pragma unroll
+  for (int st = 0; st < NSET; ++st) {
+    qa[st] = qs[st] = mq[st] = 0.f;
+    m_run[st] = -INFINITY;
+    l_run[st] = vmt[st] = 0.f;
+  }
   floatx4 acc[CB][4];                  // PV: [block][E.lo, E.hi, O.lo, O.hi]
 
-  // Query of a new segment: read the lane's 16 dims per k-block straight from
-  // the query slot, scale head hq to 31-bit integers, and cut limb lx.
-  auto begin = [&]() {
-    m_run = -INFINITY;
-    l_run = 0.f;
-    vmt = 0.f;
-#pragma unroll
-    for (int c = 0; c < CB; ++c)
-#pragma unroll
-      for (int k = 0; k < 4; ++k) acc[c][k] = floatx4{0.f, 0.f, 0.f, 0.f};
+  // Query of head set st for a new segment: read the lane's 16 dims per k-block
+  // straight from the query slot (with the token split, set st's heads are in
+  // the slot of wave 2 kvw + st; else in the wave's own), scale head hq to
+  // 31-bit integers, and cut limb lx.
+  auto begin_set = [&](int st) {
+    m_run[st] = -INFINITY;
+    l_run[st] = 0.f;
+    vmt[st] = 0.f;
+    const uint8_t* const qs_slot = TS ? smem + S::QOFF + (2 * kvw + st) * 1024 : qsl;
     float qv[KB][16];
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
         // dims kbase(kb) + 8 u .. + 7
-        const uint4 w = *reinterpret_cast<const uint4*>(qsl + 64 * ((kbase(kb) >> 3) + u) + 16 * hq);
+        const uint4 w = *reinterpret_cast<const uint4*>(qs_slot + 64 * ((kbase(kb) >> 3) + u) + 16 * hq);
         const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -316,7 +345,7 @@ __global__ void __launch_bounds__(NKV * WPK * 64) mfma_kernel(const AttnParams p
         const int b0 = 8 * (d >> 1) + (d & 1);
         dw[d] = bytes[b0] | (bytes[b0 + 2] << 8) | (bytes[b0 + 4] << 16) | (bytes[b0 + 6] << 24);
       }
-      qb[kb] = v4i{(int)dw[0], (int)dw[1], (int)dw[2], (int)dw[3]};
+      qb[st][kb] = v4i{(int)dw[0], (int)dw[1], (int)dw[2], (int)dw[3]};
     }
     {
       float a, b;
@@ -325,8 +354,16 @@ __global__ void __launch_bounds__(NKV * WPK * 64) mfma_kernel(const AttnParams p
       swap32(qsum, a, b);
       qsum = a + b;
     }
-    qs = qsum;
-    qa = __builtin_amdgcn_ldexpf(kC<D>, -sc);
+    qs[st] = qsum;
+    qa[st] = __builtin_amdgcn_ldexpf(kC<D>, -sc);
+  };
+  auto begin = [&]() {
+#pragma unroll
+    for (int c = 0; c < CB; ++c)
+#pragma unroll
+      for (int k = 0; k < 4; ++k) acc[c][k] = floatx4{0.f, 0.f, 0.f, 0.f};
+    begin_set(0);
+    if constexpr (NSET == 2) begin_set(1);
   };
 
   // ---------------------------------------------------------------- tile data
@@ -337,14 +374,17 @@ __global__ void __launch_bounds__(NKV * WPK * 64) mfma_kernel(const AttnParams p
   // stride start in 8 different 4-bank groups.
   // V: lane (row col, group grp) reads bytes [4 col, 4 col + 4) (head_dim 64:
   // [2 col, 2 col + 2)) of the V codes of its 8 k-slot tokens.
+  // With the token split, the wave reads only its half of the tile's tokens
+  // (row blocks and token half of the wave's 32 tokens).
   struct TileRegs {
-    uint32_t k[RB][2 * KB];     // packed codes: k-block kb in words 2 kb, 2 kb + 1
-    uint2 rl[RB];               // rulers of the lane's softmax tokens
-    uint32_t v[TH][8];          // V codes of the k-slots, per token half
+    uint32_t k[RBW][2 * KB];    // packed codes: k-block kb in words 2 kb, 2 kb + 1
+    uint2 rl[RBW];              // rulers of the lane's softmax tokens
+    uint32_t v[THW][8];         // V codes of the k-slots, per token half
   };
-  auto read_tile = [&](const uint8_t* Sb, TileRegs& R) {
+  auto read_tile = [&](const uint8_t* Sb0, TileRegs& R) {
+    const uint8_t* const Sb = Sb0 + 32 * half * S::RSTRIDE;
 #pragma unroll
-    for (int rb = 0; rb < RB; ++rb) {
+    for (int rb = 0; rb < RBW; ++rb) {
       const uint8_t* row = Sb + (16 * rb + col) * S::RSTRIDE;
       if constexpr (D == 128) {
         // a sub-row starts 8-byte aligned (136-byte slots): two 8-byte halves
@@ -362,9 +402,9 @@ __global__ void __launch_bounds__(NKV * WPK * 64) mfma_kernel(const AttnParams p
       }
     }
 #pragma unroll
-    for (int rb = 0; rb < RB; ++rb) R.rl[rb] = *reinterpret_cast<const uint2*>(Sb + (16 * rb + stok) * S::RSTRIDE + D);
+    for (int rb = 0; rb < RBW; ++rb) R.rl[rb] = *reinterpret_cast<const uint2*>(Sb + (16 * rb + stok) * S::RSTRIDE + D);
 #pragma unroll
-    for (int th = 0; th < TH; ++th)
+    for (int th = 0; th < THW; ++th)
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const uint8_t* src = Sb + (32 * th + ktok(grp, e)) * S::RSTRIDE + D / 2;
@@ -374,16 +414,20 @@ __global__ void __launch_bounds__(NKV * WPK * 64) mfma_kernel(const AttnParams p
   };
 
   // QK of one tile: 16 tokens x (head, limb) per row block, exact int32.
+  // C[st RBW + rb]: row block rb of the wave's tokens against head set st.
   auto qk = [&](const TileRegs& R, v4i (&C)[RB]) {
 #pragma unroll
-    for (int rb = 0; rb < RB; ++rb) {
-      C[rb] = v4i{0, 0, 0, 0};
+    for (int i = 0; i < RB; ++i) C[i] = v4i{0, 0, 0, 0};
+#pragma unroll
+    for (int rb = 0; rb < RBW; ++rb) {
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb) {
         const uint32_t x0 = R.k[rb][2 * kb], x1 = R.k[rb][2 * kb + 1];
         const v4i a{(int)(x0 & 0x0F0F0F0Fu), (int)((x0 >> 4) & 0x0F0F0F0Fu), (int)(x1 & 0x0F0F0F0Fu),
                     (int)((x1 >> 4) & 0x0F0F0F0Fu)};
-        C[rb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, qb[kb], C[rb], 0, 0, 0);
+#pragma unroll
+        for (int st = 0; st < NSET; ++st)
+          C[st * RBW + rb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, qb[st][kb], C[st * RBW + rb], 0, 0, 0);
       }
     }
   };
@@ -439,46 +483,72 @@ __global__ void __launch_bounds__(NKV * WPK * 64) mfma_kernel(const AttnParams p
   // value of head `col` (0..3) for the PV lanes: from lane 4 col, which holds head col
   auto for_pv_lane = [&](float v) {
     const float v0 = readlane_f(v, 0), v1 = readlane_f(v, 4), v2 = readlane_f(v, 8), v3 = readlane_f(v, 12);
-    return col == 0 ? v0 : col == 1 ? v1 : col == 2 ? v2 : v3;
+    const int c = col & 3;
+    return c == 0 ? v0 : c == 1 ? v1 : c == 2 ? v2 : v3;
+  };
+  // value of head `col` (0..HPW-1) for the PV lanes: head col & 3 of set col >> 2
+  auto for_pv_lane_set = [&](const float (&v)[NSET]) {
+    if constexpr (NSET == 1) {
+      return for_pv_lane(v[0]);
+    } else {
+      const float a = for_pv_lane(v[0]), b = for_pv_lane(v[1]);
+      return (col & 4) ? b : a;
+    }
   };
 
   // Softmax of one tile and its weights into the scratch.  Tokens past the
-  // sequence end get u = -inf (weight 0) and zero rulers.
+  // sequence end get u = -inf (weight 0) and zero rulers.  Score r is row block
+  // r % RBW of the wave's tokens for head set r / RBW.
   auto softmax = [&](const TileRegs& R, const float (&s)[4], int nvalid) {
     float u[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const float kmin = h2f((uint16_t)(R.rl[r].x & 0xffffu));
-      const float kstep = h2f((uint16_t)(R.rl[r].x >> 16));
-      const float sc = __builtin_fmaf(s[r], kstep, kmin * qs);
-      u[r] = 16 * r + stok < nvalid ? sc : -INFINITY;
+      const int st = r / RBW, rb = r % RBW;
+      const float kmin = h2f((uint16_t)(R.rl[rb].x & 0xffffu));
+      const float kstep = h2f((uint16_t)(R.rl[rb].x >> 16));
+      const float sc = __builtin_fmaf(s[r], kstep, kmin * qs[st]);
+      u[r] = 32 * half + 16 * rb + stok < nvalid ? sc : -INFINITY;
     }
-    const float tl = fmaxf(fmaxf(u[0], u[1]), fmaxf(u[2], u[3]));
-    if (__builtin_amdgcn_ballot_w64(tl > m_run)) {
-      const float tmax = head_max(tl);
-      const bool grow = tmax > m_run;
-      const float alpha = grow ? __builtin_amdgcn_exp2f((m_run - tmax) * qa) : 1.f;   // 0 from -inf
-      l_run *= alpha;
-      vmt *= alpha;
-      const float ap = for_pv_lane(alpha);
+    float alpha[NSET];
+    bool grew = false;
+#pragma unroll
+    for (int st = 0; st < NSET; ++st) {
+      float tl = u[st * RBW];
+#pragma unroll
+      for (int rb = 1; rb < RBW; ++rb) tl = fmaxf(tl, u[st * RBW + rb]);
+      alpha[st] = 1.f;
+      if (__builtin_amdgcn_ballot_w64(tl > m_run[st])) {
+        const float tmax = head_max(tl);
+        const bool grow = tmax > m_run[st];
+        alpha[st] = grow ? __builtin_amdgcn_exp2f((m_run[st] - tmax) * qa[st]) : 1.f;   // 0 from -inf
+        l_run[st] *= alpha[st];
+        vmt[st] *= alpha[st];
+        m_run[st] = grow ? tmax : m_run[st];
+        mq[st] = m_run[st] * qa[st];
+        grew = true;
+      }
+    }
+    if (grew) {
+      const float ap = for_pv_lane_set(alpha);
 #pragma unroll
       for (int c = 0; c < CB; ++c)
 #pragma unroll
         for (int k = 0; k < 4; ++k) acc[c][k] *= ap;
-      m_run = grow ? tmax : m_run;
-      mq = m_run * qa;
     }
     uint32_t wv[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      // m_run > -inf here: token 0 of every tile is valid
-      const float pr = __builtin_amdgcn_exp2f(__builtin_fmaf(u[r], qa, -mq));
-      float vmin = h2f((uint16_t)(R.rl[r].y & 0xffffu));
-      float vstep = h2f((uint16_t)(R.rl[r].y >> 16));
+      const int st = r / RBW, rb = r % RBW;
+      // tokens past the end give exp2(-inf) = 0 (mq is finite: the first half's
+      // token 0 is valid in every tile, and a second half without valid tokens
+      // keeps the previous finite mq or 0)
+      const float pr = __builtin_amdgcn_exp2f(__builtin_fmaf(u[r], qa[st], -mq[st]));
+      float vmin = h2f((uint16_t)(R.rl[rb].y & 0xffffu));
+      float vstep = h2f((uint16_t)(R.rl[rb].y >> 16));
       if (nvalid < TT) {
         // the sequence's last tile: slots past its end may hold anything (a
         // reused block), so their rulers must not reach the sums
-        const bool ok = 16 * r + stok < nvalid;
+        const bool ok = 32 * half + 16 * rb + stok < nvalid;
         vmin = ok ? vmin : 0.f;
         vstep = ok ? vstep : 0.f;
       }
@@ -487,29 +557,32 @@ __global__ void __launch_bounds__(NKV * WPK * 64) mfma_kernel(const AttnParams p
       // Steps below 2^-10 keep pr: there the difference moves the output by
       // less than 2^-22 of the token's weight.
       const float pp = vstep >= 0x1p-10f ? h2f((uint16_t)w) * __builtin_amdgcn_rcpf(vstep) : pr;
-      l_run += pp;
-      vmt = __builtin_fmaf(pp, vmin, vmt);
+      l_run[st] += pp;
+      vmt[st] = __builtin_fmaf(pp, vmin, vmt[st]);
       wv[r] = w;
     }
-    // token 16 r + stok: token half r >> 1, local 16 (r & 1) + stok
-    uint16_t* wh = reinterpret_cast<uint16_t*>(wscr) + hq * TT;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) wh[32 * (r >> 1) + wpos(16 * (r & 1) + stok)] = (uint16_t)wv[r];
+    for (int r = 0; r < 4; ++r) {
+      const int st = r / RBW, rb = r % RBW;
+      uint16_t* wh = reinterpret_cast<uint16_t*>(wscr) + (4 * st + hq) * TTW;
+      // token 16 rb + stok of the wave's tokens: token half rb >> 1, local 16 (rb & 1) + stok
+      wh[32 * (rb >> 1) + wpos(16 * (rb & 1) + stok)] = (uint16_t)wv[r];
+    }
   };
 
   // PV of one tile from its V byte pairs and the weights in the scratch.
   auto pv = [&](const TileRegs& R) {
     wave_lds_sync();
-    half8 bw[TH];
+    half8 bw[THW];
 #pragma unroll
-    for (int th = 0; th < TH; ++th) {
-      const uint8_t* src = col < 4 ? wscr + (col * TT + 32 * th + 8 * grp) * 2 : smem + S::ZOFF + 64 * th + 16 * grp;
+    for (int th = 0; th < THW; ++th) {
+      const uint8_t* src = col < HPW ? wscr + (col * TTW + 32 * th + 8 * grp) * 2 : smem + S::ZOFF + 64 * th + 16 * grp;
       bw[th] = *reinterpret_cast<const half8*>(src);
     }
 #pragma unroll
     for (int c = 0; c < CB; ++c)
 #pragma unroll
-      for (int th = 0; th < TH; ++th) {
+      for (int th = 0; th < THW; ++th) {
         uint32_t el[4], eh[4], ol[4], oh[4];
 #pragma unroll
         for (int d = 0; d < 4; ++d) {
@@ -545,11 +618,55 @@ __global__ void __launch_bounds__(NKV * WPK * 64) mfma_kernel(const AttnParams p
   float2 pml = make_float2(0.f, 0.f);
   int pk = 0;                          // pending stores: 0 none, 1 output, 2 partial piece
   int64_t pofs = 0, pmlofs = 0;
-  auto finish = [&](int b, int seg_first, bool whole, bool last_of_seq) {
-    const float lt = for_pv_lane(head_sum(l_run));
-    const float vt = for_pv_lane(head_sum(vmt));
-    const float mt = for_pv_lane(m_run * qa);
-    const int h = hw + (col & 3);      // lanes col >= 4 hold no output
+  auto finish = [&](int b, int seg_first, bool whole, bool last_of_seq) __attribute__((always_inline)) {
+    float lh[NSET], vh[NSET], mh[NSET];
+#pragma unroll
+    for (int st = 0; st < NSET; ++st) {
+      lh[st] = head_sum(l_run[st]);
+      vh[st] = head_sum(vmt[st]);
+      mh[st] = m_run[st] * qa[st];
+    }
+    float lt = for_pv_lane_set(lh);
+    float vt = for_pv_lane_set(vh);
+    float mt = for_pv_lane_set(mh);
+    const int h = hw + (col & (HPW - 1));   // lanes col >= HPW hold no output
+    if constexpr (TS) {
+      // The second wave of the pair hands its sums to the first, which scales
+      // both by exp2(m - max) and stores the 8 heads; the second stores nothing.
+      float* const cb = reinterpret_cast<float*>(smem + S::COFF + kvw * S::CBW);
+      float* const cml = cb + (D / 4) * 64;
+      if (half == 1) {
+#pragma unroll
+        for (int c = 0; c < CB; ++c)
+#pragma unroll
+          for (int k = 0; k < 4; ++k)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) cb[((4 * c + k) * 4 + r) * 64 + lane] = acc[c][k][r];
+        if (grp == 0 && col < 8) {
+          cml[col] = mt;
+          cml[8 + col] = lt;
+          cml[16 + col] = vt;
+        }
+      }
+      lds_barrier();
+      if (half == 1) {
+        pk = 0;
+        return;
+      }
+      const float m1 = cml[col & 7], l1 = cml[8 + (col & 7)], v1 = cml[16 + (col & 7)];
+      const float M = fmaxf(mt, m1);            // mt is finite: token 0 of every tile is the first wave's
+      const float f0 = __builtin_amdgcn_exp2f(mt - M), f1 = __builtin_amdgcn_exp2f(m1 - M);   // m1 = -inf gives 0
+#pragma unroll
+      for (int c = 0; c < CB; ++c)
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            acc[c][k][r] = __builtin_fmaf(acc[c][k][r], f0, f1 * cb[((4 * c + k) * 4 + r) * 64 + lane]);
+      lt = __builtin_fmaf(lt, f0, f1 * l1);
+      vt = __builtin_fmaf(vt, f0, f1 * v1);
+      mt = M;
+    }
     const bool final_out = whole && last_of_seq;
     const float rL = final_out ? __builtin_amdgcn_rcpf(lt) : 1.0f;
 #pragma unroll
@@ -575,7 +692,7 @@ __global__ void __launch_bounds__(NKV * WPK * 64) mfma_kernel(const AttnParams p
   };
   auto flush = [&]() {
     if (pk == 0) return;
-    if (col < 4) {
+    if (col < HPW) {
 #pragma unroll
       for (int c = 0; c < CB; ++c)
 #pragma unroll
