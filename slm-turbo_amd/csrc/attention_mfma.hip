@@ -26,10 +26,11 @@
 // QK, exact: v_mfma_i32_16x16x64_i8.  The fp16 query of each head is scaled by a
 // power of two to a 31-bit integer Q (every fp16 value above 2^-21 of the head's
 // largest is exact) and split into four signed 8-bit limbs, Q = sum_x L_x 2^(8x);
-// the 16 columns of B are (head h, limb x), the rows of A 16 tokens whose codes
-// are unpacked from nibbles to bytes.  Integer accumulation is exact; the limbs
-// are combined in fp32 while a quad reduce-scatter hands row block x to limb lane
-// x.  q.K = step * (Q.n) 2^-S + min * sum(q).
+// the 16 rows of A are (head h, limb x), the columns of B 16 tokens whose codes
+// are unpacked from nibbles to bytes.  Integer accumulation is exact, and each
+// lane of C then holds all four limbs of one (head, token): limbs 0 + 1 and
+// 2 + 3 join in int32, the two halves in one fp32 fma, with no cross-lane
+// traffic.  q.K = step * (Q.n) 2^-S + min * sum(q).
 //
 // PV: v_mfma_f32_16x16x32_f16 with A = V^T (rows: 16 V bytes, one of their two
 // nibbles; k: 32 tokens) and B = the fp16 weights (columns: the wave's 4 heads).
@@ -265,19 +266,19 @@ __global__ void __launch_bounds__(NKV * WPK * 64) mfma_kernel(const AttnParams p
 
   // ---------------------------------------------------------------- lane roles
   // col = lane & 15, grp = lane >> 4.
-  //  QK B / C and softmax: column col = 4 h + x is limb x of head h (h = col >> 2);
-  //    after the combine, the lane owns row block x: tokens 16 x + 4 grp + r of head h.
-  //  QK A: row col (token 16 rb + col), k-set grp.
+  //  QK A: row col = 4 h + x is limb x of head h (h = col >> 2), k-set grp.
+  //  QK B: column col (token 16 rb + col), k-set grp.
+  //  QK C and softmax: column col, rows 4 grp + x: the lane holds the four limbs
+  //    of head grp for token 16 rb + col of each row block.
   //  PV A: row col (V byte 32 cb + 2 col, and the next byte), k-set grp;
   //    PV B / C: column col (head col for col < 4), C rows 4 grp + r.
   const int col = lane & 15, grp = lane >> 4;
   const int hq = col >> 2, lx = col & 3;
-  const int stok = 4 * grp + lx;            // the lane's softmax tokens: 16 rb + stok
   // first of the 16 dims that k-block kb of lane group grp covers (QK)
   auto kbase = [&](int kb) { return D == 128 ? 32 * grp + 16 * kb : 16 * grp; };
   const uint8_t* const qsl = smem + S::QOFF + wave * 1024;
 
-  v4i qb[NSET][KB];                    // B operand: limb lx of head set st's head hq, k-set grp
+  v4i qb[NSET][KB];                    // A operand: limb lx of head set st's head hq, k-set grp
   float qa[NSET], qs[NSET], mq[NSET], m_run[NSET], l_run[NSET], vmt[NSET];
 #pragma unroll
   for (int st = 0; st < NSET; ++st) {
@@ -287,11 +288,17 @@ __global__ void __launch_bounds__(NKV * WPK * 64) mfma_kernel(const AttnParams p
   }
   floatx4 acc[CB][4];                  // PV: [block][E.lo, E.hi, O.lo, O.hi]
 
+  // Value of head grp for the softmax lanes, from lane 4 grp (which holds head
+  // grp in the query operand's layout).
+  auto for_soft_lane = [&](float v) {
+    const float v0 = readlane_f(v, 0), v1 = readlane_f(v, 4), v2 = readlane_f(v, 8), v3 = readlane_f(v, 12);
+    return grp == 0 ? v0 : grp == 1 ? v1 : grp == 2 ? v2 : v3;
+  };
   // Query of head set st for a new segment: read the lane's 16 dims per k-block
   // straight from the query slot (with the token split, set st's heads are in
   // the slot of wave 2 kvw + st; else in the wave's own), scale head hq to
   // 31-bit integers, and cut limb lx.
-  auto begin_set = [&](int st) {
+  auto begin_set = [&](int st) __attribute__((always_inline)) {
     m_run[st] = -INFINITY;
     l_run[st] = 0.f;
     vmt[st] = 0.f;
@@ -354,10 +361,10 @@ __global__ void __launch_bounds__(NKV * WPK * 64) mfma_kernel(const AttnParams p
       swap32(qsum, a, b);
       qsum = a + b;
     }
-    qs[st] = qsum;
-    qa[st] = __builtin_amdgcn_ldexpf(kC<D>, -sc);
+    qs[st] = for_soft_lane(qsum);
+    qa[st] = for_soft_lane(__builtin_amdgcn_ldexpf(kC<D>, -sc));
   };
-  auto begin = [&]() {
+  auto begin = [&]() __attribute__((always_inline)) {
 #pragma unroll
     for (int c = 0; c < CB; ++c)
 #pragma unroll
@@ -402,7 +409,7 @@ __global__ void __launch_bounds__(NKV * WPK * 64) mfma_kernel(const AttnParams p
       }
     }
 #pragma unroll
-    for (int rb = 0; rb < RBW; ++rb) R.rl[rb] = *reinterpret_cast<const uint2*>(Sb + (16 * rb + stok) * S::RSTRIDE + D);
+    for (int rb = 0; rb < RBW; ++rb) R.rl[rb] = *reinterpret_cast<const uint2*>(Sb + (16 * rb + col) * S::RSTRIDE + D);
 #pragma unroll
     for (int th = 0; th < THW; ++th)
 #pragma unroll
@@ -427,62 +434,40 @@ __global__ void __launch_bounds__(NKV * WPK * 64) mfma_kernel(const AttnParams p
                     (int)((x1 >> 4) & 0x0F0F0F0Fu)};
 #pragma unroll
         for (int st = 0; st < NSET; ++st)
-          C[st * RBW + rb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, qb[st][kb], C[st * RBW + rb], 0, 0, 0);
+          C[st * RBW + rb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(qb[st][kb], a, C[st * RBW + rb], 0, 0, 0);
       }
     }
   };
 
-  // Limb combine and quad reduce-scatter: C[rb][r] of lane x is limb x of token
-  // 16 rb + 4 grp + r; the partner across lane bit 1 takes the other pair of
-  // rows, the partner across bit 0 the other row of the pair, so s[rb] = Q.n of
-  // token 16 rb + stok, head hq, summed over the 4 limbs.
+  // Limb combine: C[r] of lane (col, grp) holds limbs 0..3 of head grp for
+  // token 16 rb + col (r = st RBW + rb).  Each limb sum is below 2^18 in
+  // magnitude (128 dims x 128 x 15), so limbs 0 + 1 and 2 + 3 join exactly in
+  // int32 and s = lo + 2^16 hi = Q.n rounds once per half and once in the fma.
   auto combine = [&](const v4i (&C)[RB], float (&s)[4]) {
-    const float lsc = __builtin_amdgcn_ldexpf(1.0f, 8 * lx);
-    float f[4][4];
 #pragma unroll
-    for (int rb = 0; rb < 4; ++rb)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) f[rb][r] = (float)C[rb][r] * lsc;
-    const bool b1 = lx & 2, b0 = lx & 1;
-    float t[4][2];
-#pragma unroll
-    for (int rb = 0; rb < 4; ++rb)
-#pragma unroll
-      for (int k = 0; k < 2; ++k) {
-        const float keep = b1 ? f[rb][2 + k] : f[rb][k];
-        const float send = b1 ? f[rb][k] : f[rb][2 + k];
-        t[rb][k] = keep + dpp_f<DPP_QUAD_XOR2>(send);
-      }
-#pragma unroll
-    for (int rb = 0; rb < 4; ++rb) {
-      const float keep = b0 ? t[rb][1] : t[rb][0];
-      const float send = b0 ? t[rb][0] : t[rb][1];
-      s[rb] = keep + dpp_f<DPP_QUAD_XOR1>(send);
+    for (int r = 0; r < 4; ++r) {
+      const int lo = (int)((uint32_t)C[r][0] + ((uint32_t)C[r][1] << 8));
+      const int hi = (int)((uint32_t)C[r][2] + ((uint32_t)C[r][3] << 8));
+      s[r] = __builtin_fmaf((float)hi, 65536.0f, (float)lo);
     }
   };
 
-  // Sum / max over the 16 lanes of head hq (quad and rows).
+  // Sum / max over the 16 lanes of head grp (one row of the wave).
   auto head_max = [&](float v) {
-    v = fmaxf(v, dpp_f<DPP_QUAD_XOR1>(v));
+    v = fmaxf(v, dpp_f<DPP_ROW_ROR8>(v));
+    v = fmaxf(v, dpp_f<DPP_ROW_ROR4>(v));
     v = fmaxf(v, dpp_f<DPP_QUAD_XOR2>(v));
-    float a, b;
-    swap16(v, a, b);
-    v = fmaxf(a, b);
-    swap32(v, a, b);
-    return fmaxf(a, b);
+    return fmaxf(v, dpp_f<DPP_QUAD_XOR1>(v));
   };
   auto head_sum = [&](float v) {
-    v += dpp_f<DPP_QUAD_XOR1>(v);
+    v += dpp_f<DPP_ROW_ROR8>(v);
+    v += dpp_f<DPP_ROW_ROR4>(v);
     v += dpp_f<DPP_QUAD_XOR2>(v);
-    float a, b;
-    swap16(v, a, b);
-    v = a + b;
-    swap32(v, a, b);
-    return a + b;
+    return v + dpp_f<DPP_QUAD_XOR1>(v);
   };
-  // value of head `col` (0..3) for the PV lanes: from lane 4 col, which holds head col
+  // value of head `col` (0..3) for the PV lanes: from lane 16 col, which holds head col
   auto for_pv_lane = [&](float v) {
-    const float v0 = readlane_f(v, 0), v1 = readlane_f(v, 4), v2 = readlane_f(v, 8), v3 = readlane_f(v, 12);
+    const float v0 = readlane_f(v, 0), v1 = readlane_f(v, 16), v2 = readlane_f(v, 32), v3 = readlane_f(v, 48);
     const int c = col & 3;
     return c == 0 ? v0 : c == 1 ? v1 : c == 2 ? v2 : v3;
   };
@@ -507,7 +492,7 @@ __global__ void __launch_bounds__(NKV * WPK * 64) mfma_kernel(const AttnParams p
       const float kmin = h2f((uint16_t)(R.rl[rb].x & 0xffffu));
       const float kstep = h2f((uint16_t)(R.rl[rb].x >> 16));
       const float sc = __builtin_fmaf(s[r], kstep, kmin * qs[st]);
-      u[r] = 32 * half + 16 * rb + stok < nvalid ? sc : -INFINITY;
+      u[r] = 32 * half + 16 * rb + col < nvalid ? sc : -INFINITY;
     }
     float alpha[NSET];
     bool grew = false;
@@ -548,7 +533,7 @@ __global__ void __launch_bounds__(NKV * WPK * 64) mfma_kernel(const AttnParams p
       if (nvalid < TT) {
         // the sequence's last tile: slots past its end may hold anything (a
         // reused block), so their rulers must not reach the sums
-        const bool ok = 32 * half + 16 * rb + stok < nvalid;
+        const bool ok = 32 * half + 16 * rb + col < nvalid;
         vmin = ok ? vmin : 0.f;
         vstep = ok ? vstep : 0.f;
       }
@@ -564,9 +549,9 @@ __global__ void __launch_bounds__(NKV * WPK * 64) mfma_kernel(const AttnParams p
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int st = r / RBW, rb = r % RBW;
-      uint16_t* wh = reinterpret_cast<uint16_t*>(wscr) + (4 * st + hq) * TTW;
-      // token 16 rb + stok of the wave's tokens: token half rb >> 1, local 16 (rb & 1) + stok
-      wh[32 * (rb >> 1) + wpos(16 * (rb & 1) + stok)] = (uint16_t)wv[r];
+      uint16_t* wh = reinterpret_cast<uint16_t*>(wscr) + (4 * st + grp) * TTW;
+      // token 16 rb + col of the wave's tokens: token half rb >> 1, local 16 (rb & 1) + col
+      wh[32 * (rb >> 1) + wpos(16 * (rb & 1) + col)] = (uint16_t)wv[r];
     }
   };
 
@@ -690,7 +675,7 @@ __global__ void __launch_bounds__(NKV * WPK * 64) mfma_kernel(const AttnParams p
       pml = make_float2(mt, lt);
     }
   };
-  auto flush = [&]() {
+  auto flush = [&]() __attribute__((always_inline)) {
     if (pk == 0) return;
     if (col < HPW) {
 #pragma unroll

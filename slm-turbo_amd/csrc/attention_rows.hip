@@ -827,7 +827,12 @@ bool rows_shape(int H, int G, int D, int cache_kv, int* nkv, int* wpk, int* grou
   if (cache_kv != KV || cache_kv % 2 != 0) return false;
   const int w = G / 4;
   int n = 0;
+  // Two waves per KV head: at head_dim 64 two KV heads per workgroup (4 waves,
+  // three workgroups per CU) keep more independent waves on each SIMD than
+  // four (8 waves, one workgroup per CU by registers); at 128 the reverse
+  // measured faster.
   if (w == 1) n = KV % 8 == 0 ? 8 : KV % 4 == 0 ? 4 : KV % 2 == 0 ? 2 : 0;
+  else if (D == 64) n = KV % 2 == 0 ? 2 : 0;
   else n = KV % 4 == 0 ? 4 : KV % 2 == 0 ? 2 : 0;
   if (n == 0) return false;
   *nkv = n;
@@ -847,7 +852,8 @@ bool rows_shape(int H, int G, int D, int cache_kv, int* nkv, int* wpk, int* grou
 // Workgroups per head group the whole-row kernel may use (its workspace bound).
 int rows_max_workgroups(int D, int nkv, int wpk, int groups, int cus) {
   const int waves = nkv * wpk;
-  // at most 8 waves per CU (up to 256 VGPRs each), and the ring's LDS
+  // at most 8 waves per CU at head_dim 128 (up to 256 VGPRs each), 12 at 64
+  // (up to 168), and the ring's LDS
   size_t lds = 0;
   switch (SLMT_ROWS_KEY(D, nkv, wpk)) {
 #define SLMT_ROWS_LDS(d, a, b, c) case SLMT_ROWS_KEY(d, a, b): lds = rows::Shape<d, a, b, c>::LDS; break;
@@ -855,7 +861,7 @@ int rows_max_workgroups(int D, int nkv, int wpk, int groups, int cus) {
 #undef SLMT_ROWS_LDS
     default: return 1;
   }
-  int per_cu = std::min(8 / waves, (int)((160 * 1024) / lds));
+  int per_cu = std::min((D == 64 ? 12 : 8) / waves, (int)((160 * 1024) / lds));
   per_cu = std::max(1, per_cu);
   return std::max(1, cus * per_cu / groups);
 }
