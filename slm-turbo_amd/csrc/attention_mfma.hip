@@ -486,13 +486,26 @@ __global__ void __launch_bounds__(NKV * WPK * 64) mfma_kernel(const AttnParams p
   // r % RBW of the wave's tokens for head set r / RBW.
   auto softmax = [&](const TileRegs& R, const float (&s)[4], int nvalid) {
     float u[4];
+    uint32_t vr[RBW];                  // V rulers (min, step) of the lane's tokens, fp16 pair
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int st = r / RBW, rb = r % RBW;
-      const float kmin = h2f((uint16_t)(R.rl[rb].x & 0xffffu));
-      const float kstep = h2f((uint16_t)(R.rl[rb].x >> 16));
-      const float sc = __builtin_fmaf(s[r], kstep, kmin * qs[st]);
-      u[r] = 32 * half + 16 * rb + col < nvalid ? sc : -INFINITY;
+      const uint32_t kr = R.rl[rb].x;
+      u[r] = __builtin_fmaf(s[r], h2f((uint16_t)(kr >> 16)), h2f((uint16_t)(kr & 0xffffu)) * qs[st]);
+    }
+#pragma unroll
+    for (int rb = 0; rb < RBW; ++rb) vr[rb] = R.rl[rb].y;
+    if (nvalid < TT) {
+      // the sequence's last tile: slots past its end may hold anything (a
+      // reused block), so they get u = -inf and their rulers must not reach
+      // the sums
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int rb = r % RBW;
+        u[r] = 32 * half + 16 * rb + col < nvalid ? u[r] : -INFINITY;
+      }
+#pragma unroll
+      for (int rb = 0; rb < RBW; ++rb) vr[rb] = 32 * half + 16 * rb + col < nvalid ? vr[rb] : 0u;
     }
     float alpha[NSET];
     bool grew = false;
@@ -528,22 +541,16 @@ __global__ void __launch_bounds__(NKV * WPK * 64) mfma_kernel(const AttnParams p
       // token 0 is valid in every tile, and a second half without valid tokens
       // keeps the previous finite mq or 0)
       const float pr = __builtin_amdgcn_exp2f(__builtin_fmaf(u[r], qa[st], -mq[st]));
-      float vmin = h2f((uint16_t)(R.rl[rb].y & 0xffffu));
-      float vstep = h2f((uint16_t)(R.rl[rb].y >> 16));
-      if (nvalid < TT) {
-        // the sequence's last tile: slots past its end may hold anything (a
-        // reused block), so their rulers must not reach the sums
-        const bool ok = 32 * half + 16 * rb + col < nvalid;
-        vmin = ok ? vmin : 0.f;
-        vstep = ok ? vstep : 0.f;
-      }
-      const uint32_t w = f2h(pr * vstep);
+      const float vstep = h2f((uint16_t)(vr[rb] >> 16));
+      const _Float16 wh = (_Float16)(pr * vstep);
+      const uint32_t w = __builtin_bit_cast(uint16_t, wh);
       // P.V applies w; the sums take the probability it stands for, w / step.
-      // Steps below 2^-10 keep pr: there the difference moves the output by
-      // less than 2^-22 of the token's weight.
-      const float pp = vstep >= 0x1p-10f ? h2f((uint16_t)w) * __builtin_amdgcn_rcpf(vstep) : pr;
+      // Steps below 2^-10 (fp16 bits below 0x1400; steps are not negative)
+      // keep pr: there the difference moves the output by less than 2^-22 of
+      // the token's weight.
+      const float pp = (int)vr[rb] >= 0x14000000 ? (float)wh * __builtin_amdgcn_rcpf(vstep) : pr;
       l_run[st] += pp;
-      vmt[st] = __builtin_fmaf(pp, vmin, vmt[st]);
+      vmt[st] = __builtin_fmaf(pp, h2f((uint16_t)(vr[rb] & 0xffffu)), vmt[st]);
       wv[r] = w;
     }
 #pragma unroll
