@@ -38,7 +38,10 @@
 // once hit 8 disjoint bank groups), V^T as [dim][key] fp16 rows padded to 136
 // bytes (8-byte reads of 16 rows hit 16 disjoint bank pairs).  The next tile's
 // codes are loaded into registers two tiles ahead and written to LDS after the
-// current tile's products; one barrier per tile.
+// current tile's products; one barrier per tile.  Within a tile, all K operand
+// reads are issued before the first QK product and all V^T operand reads
+// before the softmax, so LDS latency hides behind the products and the
+// exponentials instead of stalling each product.
 #include "slmt_internal.h"
 
 #include <type_traits>
@@ -85,8 +88,10 @@ __device__ __forceinline__ uint32_t nib_pair(uint32_t lo_all, uint32_t hi_all, i
 
 // HP query heads of one KV head per workgroup (4 waves each, the same 64 query
 // rows): the K/V tiles are staged once, by the first four waves, for all of them.
+// Head_dim 64 is held to 128 VGPRs, four waves per SIMD (two 8-wave workgroups
+// per CU).
 template <int D, int HP>
-__global__ void __launch_bounds__(256 * HP) prefill_kernel(const Params p) {
+__global__ void __launch_bounds__(256 * HP) __attribute__((amdgpu_waves_per_eu(D == 64 ? 4 : 1))) prefill_kernel(const Params p) {
   using GG = Geo<D>;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const int tid = threadIdx.x, lane = tid & 63, w = (tid >> 6) & 3;
@@ -126,12 +131,20 @@ __global__ void __launch_bounds__(256 * HP) prefill_kernel(const Params p) {
   }
 
   // ---- staging roles
-  // K: thread (key kk = tid / 4, quarter ku = tid % 4): dims D/4 * ku .. + D/4 - 1
-  const int kk = tid >> 2, ku = tid & 3;
+  // K: thread (key kk, quarter ku): dims D/4 * ku .. + D/4 - 1.  Staging wave v
+  // takes keys 16 v .. 16 v + 15, lane l key 16 v + (l & 15) and quarter l >> 4:
+  // the lanes of a quarter write consecutive rows of a 36- (68-) word stride,
+  // which start 4 banks apart, and the wave's loads cover its 16 keys' codes
+  // contiguously.
+  const int kk = (tid & 15) + 16 * ((tid >> 6) & 3), ku = (tid >> 4) & 3;
   const half2v kzc = half2v{(_Float16)1024.0f, (_Float16)1024.0f};
-  // V: thread (key pair vk = tid / 8, byte group vb = tid % 8 (+ 8)): dims 8 vb .. 8 vb + 7,
-  // each with 1024 + its rounded zero point
-  const int vk = tid >> 3, vb = tid & 7;
+  // V: thread (key pair vk, byte group vb (+ 8)): dims 8 vb .. 8 vb + 7, each with
+  // 1024 + its rounded zero point.  A staging wave takes 16 key pairs x 4 byte
+  // groups, lane l key pair (l & 15) and byte group l >> 4, so that the lanes of
+  // one V^T store (row d = 8 vb + const, word vk of a 34-word row: bank
+  // 16 vb + vk + const) hit distinct banks.
+  const int vwv = (tid >> 6) & 3;
+  const int vk = (lane & 15) + 16 * (vwv & 1), vb = 4 * (vwv >> 1) + (lane >> 4);
   auto zround = [&](int d) { return quant ? fminf(fmaxf(__builtin_rintf(hf(p.vz[(int64_t)kv * D + d])), 0.f), 15.f) : 0.f; };
   half2v vzc[GG::VW][8];
 #pragma unroll
@@ -239,17 +252,37 @@ __global__ void __launch_bounds__(256 * HP) prefill_kernel(const Params p) {
     const uint8_t* Ks = smem + sl * GG::STAGE;
     const uint8_t* Vs = Ks + GG::KBYTES;
     // S^T: keys 16 n + 4 grp + i of this tile against the lane's query
+    // (all K operand reads are issued before the first product)
+    half8 ka[4][D / 32];
+#pragma unroll
+    for (int n = 0; n < 4; ++n)
+#pragma unroll
+      for (int j = 0; j < D / 32; ++j)
+        ka[n][j] = *reinterpret_cast<const half8*>(Ks + (16 * n + col) * GG::KROW + (32 * j + 8 * grp) * 2);
+    __builtin_amdgcn_sched_barrier(0);
     floatx4 s[4];
 #pragma unroll
     for (int n = 0; n < 4; ++n) {
       s[n] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int j = 0; j < D / 32; ++j) {
-        const half8 a = *reinterpret_cast<const half8*>(Ks + (16 * n + col) * GG::KROW + (32 * j + 8 * grp) * 2);
-        s[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qh[j], s[n], 0, 0, 0);
-        s[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, ql[j], s[n], 0, 0, 0);
+        s[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[n][j], qh[j], s[n], 0, 0, 0);
+        s[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[n][j], ql[j], s[n], 0, 0, 0);
       }
     }
+    // The V^T operands of the tile, read now so that their LDS latency hides
+    // behind the softmax: dims 16 c + col, keys 32 hh + 4 grp + i and
+    // 32 hh + 16 + 4 grp + i (i < 4).
+    half8 va[D / 16][2];
+#pragma unroll
+    for (int c = 0; c < D / 16; ++c)
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        const uint8_t* vrow = Vs + (16 * c + col) * GG::VROW;
+        const half4 a0 = *reinterpret_cast<const half4*>(vrow + (32 * hh + 4 * grp) * 2);
+        const half4 a1 = *reinterpret_cast<const half4*>(vrow + (32 * hh + 16 + 4 * grp) * 2);
+        va[c][hh] = __builtin_shufflevector(a0, a1, 0, 1, 2, 3, 4, 5, 6, 7);
+      }
     // Keys past S or past a causal row are masked.  A tile whose keys all lie
     // before S and at or before the wave's first row (m0 + 16 w) needs no mask:
     // the test is uniform over the wave.
@@ -273,8 +306,14 @@ __global__ void __launch_bounds__(256 * HP) prefill_kernel(const Params p) {
           tmax = fmaxf(tmax, v);
         }
     }
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+    {
+      // across the four lane groups (rows of 16 lanes) that hold the column
+      float a, b;
+      swap16(tmax, a, b);
+      tmax = fmaxf(a, b);
+      swap32(tmax, a, b);
+      tmax = fmaxf(a, b);
+    }
     // The reference maximum moves only when some column's maximum exceeds it by
     // more than 2^8 (base-2 logits): the weights then stay below 256, well inside
     // fp16, and the running sums are rescaled rarely (alpha = 0 from the initial
@@ -300,12 +339,8 @@ __global__ void __launch_bounds__(256 * HP) prefill_kernel(const Params p) {
     for (int c = 0; c < D / 16; ++c)
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) {
-        const uint8_t* vrow = Vs + (16 * c + col) * GG::VROW;
-        const half4 a0 = *reinterpret_cast<const half4*>(vrow + (32 * hh + 4 * grp) * 2);
-        const half4 a1 = *reinterpret_cast<const half4*>(vrow + (32 * hh + 16 + 4 * grp) * 2);
-        const half8 a = __builtin_shufflevector(a0, a1, 0, 1, 2, 3, 4, 5, 6, 7);
         const half8 b = __builtin_shufflevector(pb[2 * hh], pb[2 * hh + 1], 0, 1, 2, 3, 4, 5, 6, 7);
-        o[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, o[c], 0, 0, 0);
+        o[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va[c][hh], b, o[c], 0, 0, 0);
       }
 #pragma unroll
     for (int hh = 0; hh < 2; ++hh) {
