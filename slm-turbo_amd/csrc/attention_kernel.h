@@ -162,18 +162,25 @@ __device__ __forceinline__ void vm_wait_tiles(int ahead) {   // ahead wave-unifo
 // are non-temporal (nt): every cache byte is read once per decode step, and
 // the streaming policy keeps it from displacing useful lines in L2 and the
 // Infinity Cache (measured: 13 % less time for the load stream of a 303 MB
-// cache).
+// cache).  NT = false keeps the default policy, for data that a second
+// workgroup reads too.
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
+template <bool NT = true>
 __device__ __forceinline__ void lds_load16(const void* sbase, uint32_t voff, uint32_t lds) {
   // the base and the LDS address are wave-uniform; readfirstlane keeps them in
   // SGPRs even where the compiler has them in VGPRs (divergent code)
   const uint64_t b = reinterpret_cast<uint64_t>(sbase);
   const uint64_t bs = (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)b) |
                       ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(b >> 32)) << 32);
-  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1 nt" ::"v"(voff),
-               "s"(reinterpret_cast<const void*>(bs)), "s"(__builtin_amdgcn_readfirstlane(lds))
-               : "memory", "m0");
+  if constexpr (NT)
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1 nt" ::"v"(voff),
+                 "s"(reinterpret_cast<const void*>(bs)), "s"(__builtin_amdgcn_readfirstlane(lds))
+                 : "memory", "m0");
+  else
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff),
+                 "s"(reinterpret_cast<const void*>(bs)), "s"(__builtin_amdgcn_readfirstlane(lds))
+                 : "memory", "m0");
 }
 #pragma clang diagnostic pop
 

@@ -87,6 +87,14 @@ def test_decode_bytes_match_the_benchmark_formula():
     assert rl.decode_attention_bytes(lens.tolist(), 32, 8, 128, 16) == bench.algorithmic_bytes(lens)
 
 
+# Upper bound of measured / algorithmic HBM bytes per decode launch.  The
+# batch-32, 4096-key workload at head_dim 64 splits each sequence over ~12 of
+# 768 workgroups, and the (m, l, o) partials those write (3.4 MB, read back by
+# the merge kernel) are outside the algorithmic bytes; its two KV-head groups
+# also share the 64-byte line where a cache row's halves meet.
+TRAFFIC_BOUND = {"headline": 1.1, "long-context": 1.1, "full-model-attention": 1.15}
+
+
 @pytest.mark.parametrize("name", ["headline", "long-context", "full-model-attention"])
 def test_benchmark_workloads_have_traffic_summaries(name):
     """Every bench.py workload has a committed counter summary whose HBM bytes
@@ -99,7 +107,7 @@ def test_benchmark_workloads_have_traffic_summaries(name):
     alg = bench.algorithmic_bytes(lens, w)
     assert alg == rl.decode_attention_bytes(lens.tolist(), w.H, w.KV, w.D, bench.BS)
     traffic = bench.read_traffic(w)
-    assert traffic is not None and 1.0 <= traffic / alg < 1.1
+    assert traffic is not None and 1.0 <= traffic / alg < TRAFFIC_BOUND[name]
 
 
 def test_decode_attention_intensity_is_below_the_ridge():
