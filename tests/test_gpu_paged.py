@@ -138,6 +138,21 @@ def test_paged_edge_lengths_and_formats(D, paged_kernel):
     assert np.all(_run_batched(case)[[0, 6]] == 0.0)
 
 
+@pytest.mark.parametrize("H,KV,D", [(64, 8, 128), (32, 4, 64), (16, 2, 128)])
+def test_paged_edge_lengths_eight_heads_per_kv(H, KV, D, paged_kernel):
+    """8 query heads per KV head around the 32-token halves of a tile (the two
+    waves of a KV head split a tile's tokens at head_dim 128): a sequence with
+    no token in the second half, exactly one half, one token past it, and the
+    tile boundaries, mixed with long ones so sequences share workgroups."""
+    lens = [0, 1, 15, 31, 32, 33, 63, 64, 65, 95, 97, 2000, 5000, 0, 2]
+    case = make_paged_case(seed=H + D, B=len(lens), H=H, KV=KV, D=D, lens=lens)
+    ref = paged_reference(case)
+    got = _run_batched(case)
+    assert_close(got, ref, what=f"G=8 edge lengths H={H} D={D}")
+    assert_close(_run_batched(case, out_dtype=torch.float16), ref, what="fp16 out")
+    assert np.all(got[[0, 13]] == 0.0)
+
+
 def test_paged_student_t_long_context():
     """Config-4 shaped heads (64 q / 8 kv, D=128) with heavy-tailed K/V."""
     case = make_paged_case(seed=4, B=2, H=64, KV=8, D=128, len_range=(4000, 9000), dist="t3")
