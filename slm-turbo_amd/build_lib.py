@@ -5,7 +5,9 @@
 
 Each .hip translation unit is compiled to an object in slm-turbo_amd/_build/
 and the objects are linked into slm-turbo_amd/kernels/libslmturbo_hip.so,
-which kernels/kv_dequant.py loads through ctypes.
+which kernels/kv_dequant.py loads through ctypes.  csrc/pyfast.c becomes the
+CPython module kernels/_slmt_fast (gcc), a low-overhead binding of the two
+per-layer entry points of that same library.
 """
 from __future__ import annotations
 
@@ -14,6 +16,7 @@ import os
 import shutil
 import subprocess
 import sys
+import sysconfig
 from concurrent.futures import ThreadPoolExecutor
 from pathlib import Path
 
@@ -74,7 +77,21 @@ def build(verbose: bool = False, jobs: int | None = None) -> Path:
     tmp = LIB.with_suffix(".so.tmp")
     _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)], verbose)
     os.replace(tmp, LIB)
+    build_fastcall(verbose)
     return LIB
+
+
+def build_fastcall(verbose: bool = False) -> Path:
+    """kernels/_slmt_fast<ext>: the METH_FASTCALL binding (host C, no device code)."""
+    gcc = shutil.which("gcc") or shutil.which("cc")
+    if gcc is None:
+        raise RuntimeError("gcc not found (needed for the CPython binding kernels/_slmt_fast)")
+    out = PKG / "kernels" / ("_slmt_fast" + sysconfig.get_config_var("EXT_SUFFIX"))
+    tmp = out.with_name(out.name + ".tmp")
+    _run([gcc, "-O2", "-fPIC", "-shared", "-Wall", "-Wextra", f"-I{sysconfig.get_paths()['include']}",
+          str(CSRC / "pyfast.c"), "-o", str(tmp)], verbose)
+    os.replace(tmp, out)
+    return out
 
 
 def main(argv=None) -> int:

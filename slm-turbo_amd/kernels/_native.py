@@ -86,6 +86,33 @@ def load():
         return lib
 
 
+_fast = None
+_fast_tried = False
+
+
+def fast():
+    """The CPython METH_FASTCALL binding (kernels/_slmt_fast, built from
+    csrc/pyfast.c) bound to the loaded library's slmt_quantize_store and
+    slmt_decode_paged_batched, or None when it was not built.  It calls the
+    same entry points as the ctypes functions, with less per-call overhead."""
+    global _fast, _fast_tried
+    if _fast_tried:
+        return _fast
+    lib = load()
+    with _lock:
+        if not _fast_tried:
+            try:
+                from . import _slmt_fast as mod
+            except ImportError:
+                mod = None
+            if mod is not None:
+                mod.bind(ctypes.cast(lib.slmt_quantize_store, ctypes.c_void_p).value,
+                         ctypes.cast(lib.slmt_decode_paged_batched, ctypes.c_void_p).value)
+            _fast = mod
+            _fast_tried = True
+    return _fast
+
+
 def last_error(lib) -> str:
     msg = lib.slmt_last_error()
     return msg.decode() if msg else ""

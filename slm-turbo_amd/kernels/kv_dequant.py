@@ -53,6 +53,19 @@ def _load_native_extension():
 
 
 _raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+_fast_mod = None
+_fast_checked = False
+
+
+def _fastcall():
+    """The METH_FASTCALL binding of the store and batched decode (None when it
+    was not built: the ctypes functions of the same library are used then)."""
+    global _fast_mod, _fast_checked
+    if not _fast_checked:
+        _fast_mod = _native.fast()
+        _fast_checked = True
+    return _fast_mod
+_current_device = getattr(torch._C, "_cuda_getDevice", None) or torch.cuda.current_device
 
 
 def _stream(device: torch.device) -> int:
@@ -303,20 +316,26 @@ def kv_quantize_store(key, value, kv_cache, slot_mapping, block_size):
         raise RuntimeError(f"store: value must be [N, KV, D] like key, got {list(value.shape)}")
     if len(cshape) != 4 or cshape[2] != KV or cshape[1] != block_size:
         raise RuntimeError(f"store: kv_cache must be [num_blocks, {block_size}, {KV}, {SLOT}], got {list(cshape)}")
-    dev = key.device
-    with _on_device(dev):
-        # token-strided rows are read in place; anything else is made contiguous
-        ks, vs = key.stride(), value.stride()
-        if not (ks[2] == 1 and ks[1] == D and ks[0] % 2 == 0):
-            key, ks = key.contiguous(), (KV * D,)
-        if not (vs[2] == 1 and vs[1] == D and vs[0] % 2 == 0):
-            value, vs = value.contiguous(), (KV * D,)
+    # token-strided rows are read in place; anything else is made contiguous
+    ks, vs = key.stride(), value.stride()
+    if not (ks[2] == 1 and ks[1] == D and ks[0] % 2 == 0):
+        key, ks = key.contiguous(), (KV * D,)
+    if not (vs[2] == 1 and vs[1] == D and vs[0] % 2 == 0):
+        value, vs = value.contiguous(), (KV * D,)
+    if not slot_mapping.is_contiguous():
         slot_mapping = slot_mapping.contiguous()
-        rc = lib.slmt_quantize_store(
-            key.data_ptr(), ks[0], value.data_ptr(), vs[0], kv_cache.data_ptr(), cshape[0], int(block_size),
-            slot_mapping.data_ptr(), N, KV, D, _stream(dev))
-        if rc:
-            _native.check(lib, rc)
+    di = key.get_device()
+    args = (key.data_ptr(), ks[0], value.data_ptr(), vs[0], kv_cache.data_ptr(), cshape[0], int(block_size),
+            slot_mapping.data_ptr(), N, KV, D)
+    fast = _fastcall()
+    if _raw_stream is not None and di == _current_device():
+        stream = _raw_stream(di)
+        rc = fast.quantize_store(*args, stream) if fast else lib.slmt_quantize_store(*args, stream)
+    else:
+        with torch.cuda.device(di):
+            rc = lib.slmt_quantize_store(*args, _stream(key.device))
+    if rc:
+        _native.check(lib, rc)
 
 
 # =============================================================================
@@ -423,7 +442,8 @@ def kv_dequant_decode_paged_batched(
         seq_lens = seq_lens.contiguous()
         stream = _stream(dev)
         ws, ws_bytes = _workspace(lib, dev, B, H, num_kv_heads, D, stream)
-        rc = lib.slmt_decode_paged_batched(
+        fast = _fastcall()
+        rc = (fast.decode_paged_batched if fast else lib.slmt_decode_paged_batched)(
             q.data_ptr(), qs[0], qs[1], kv_cache.data_ptr(), cshape[0], int(block_size),
             block_tables.data_ptr(), 64 if bt_dtype is torch.int64 else 32, bt_stride[0],
             seq_lens.data_ptr(), 0, B, H, num_kv_heads, D, out.data_ptr(),

@@ -67,16 +67,20 @@ def test_version_and_workspace_sizes(lib):
     assert counters * 4 <= lib.slmt_attention_workspace_bytes(0, 32, 8, 128) <= a <= b
 
 
-def _paged(lib, **kw):
+def _paged_args(**kw):
     a = dict(q=16, qs=4096, qh=128, cache=16, nb=4, bs=16, bt=16, bits=32, bts=4, sl=None, fixed=5,
              B=1, H=32, KV=8, D=128, out=16, od=_native.OUT_F32, os_=4096, oh=128, ws=None, wsb=0)
     a.update(kw)
-    return lib.slmt_decode_paged_batched(a["q"], a["qs"], a["qh"], a["cache"], a["nb"], a["bs"], a["bt"],
-                                         a["bits"], a["bts"], a["sl"], a["fixed"], a["B"], a["H"], a["KV"],
-                                         a["D"], a["out"], a["od"], a["os_"], a["oh"], a["ws"], a["wsb"], None)
+    return [a["q"], a["qs"], a["qh"], a["cache"], a["nb"], a["bs"], a["bt"], a["bits"], a["bts"], a["sl"],
+            a["fixed"], a["B"], a["H"], a["KV"], a["D"], a["out"], a["od"], a["os_"], a["oh"], a["ws"],
+            a["wsb"], None]
 
 
-@pytest.mark.parametrize("kw,msg", [
+def _paged(lib, **kw):
+    return lib.slmt_decode_paged_batched(*_paged_args(**kw))
+
+
+PAGED_VALIDATION = [
     (dict(D=96), b"head_dim must be 64/80/128"),
     (dict(KV=6), b"H not divisible by num_kv_heads"),
     (dict(bs=0), b"block_size must be positive"),
@@ -87,7 +91,10 @@ def _paged(lib, **kw):
     (dict(q=None), b"null pointer argument"),
     (dict(q=8), b"q must be 16-byte aligned"),
     (dict(qh=100), b"q must be 16-byte aligned"),
-])
+]
+
+
+@pytest.mark.parametrize("kw,msg", PAGED_VALIDATION)
 def test_paged_decode_validation(lib, kw, msg):
     assert _paged(lib, **kw) == _native.ERR_INVALID
     assert msg in lib.slmt_last_error()
@@ -141,3 +148,37 @@ def test_contiguous_entry_points_validate_block_sizes(lib):
     assert lib.slmt_decode_per_channel(f, f, f, f, f, f, f, 8, 2, 2, 4, 64, 16, 1, f, None, 0, None) \
         == _native.ERR_INVALID
     assert b"kv_dequant_decode: BLOCK_N must be 32 or 64" in lib.slmt_last_error()
+
+
+def _fast(lib):
+    f = _native.fast()
+    if f is None:
+        pytest.fail("kernels/_slmt_fast is not built: run `python slm-turbo_amd/build_lib.py`")
+    return f
+
+
+@pytest.mark.parametrize("kw,msg", PAGED_VALIDATION)
+def test_fastcall_decode_reaches_the_same_checks(lib, kw, msg):
+    """The METH_FASTCALL binding passes all 22 arguments through unchanged:
+    each bad one is rejected by the library with the same status and message
+    as through ctypes (None is the null pointer 0 there)."""
+    f = _fast(lib)
+    args = [0 if v is None else v for v in _paged_args(**kw)]
+    assert f.decode_paged_batched(*args) == _native.ERR_INVALID
+    assert msg in lib.slmt_last_error()
+    assert f.decode_paged_batched(*[0 if v is None else v for v in _paged_args(B=0, q=None, out=None)]) == _native.OK
+
+
+def test_fastcall_store_reaches_the_same_checks(lib):
+    f = _fast(lib)
+    assert f.quantize_store(16, 1024, 16, 1024, 16, 4, 16, 16, 1, 8, 96, 0) == _native.ERR_INVALID
+    assert b"store: head_dim must be 64/80/128" in lib.slmt_last_error()
+    assert f.quantize_store(16, 100, 16, 1024, 16, 4, 16, 16, 1, 8, 128, 0) == _native.ERR_INVALID
+    assert b"token stride smaller than KV*D" in lib.slmt_last_error()
+    assert f.quantize_store(0, 1024, 0, 1024, 0, 4, 16, 0, 0, 8, 128, 0) == _native.OK
+    with pytest.raises(TypeError):
+        f.quantize_store(1, 2, 3)
+    with pytest.raises(TypeError):
+        f.quantize_store("x", 1024, 16, 1024, 16, 4, 16, 16, 1, 8, 128, 0)
+    with pytest.raises(TypeError):
+        f.decode_paged_batched(*range(21))
