@@ -379,19 +379,13 @@ __device__ bool schedule_range(const AttnParams& p, int* misc, int h0, int h1, T
 // thread merges IPT items at once, MB pieces per batch, with all of a batch's
 // loads issued together, and updates the running maximum once per batch.  For
 // the per-channel layout the V scale/zero are applied to the merged average.
-// IN_KERNEL: the pieces come from workgroups of the running kernel (read
-// agent-coherently, arrival counter re-armed at the end); otherwise from a
-// kernel that ran before this one on the same stream (plain loads, 8 pieces
-// per batch).
-template <int D, int MODE, bool IN_KERNEL = true>
+// The arrival counter is re-armed at the end.
+template <int D, int MODE>
 __device__ void merge_sequence(const AttnParams& p, int b, int Pb, int Tb, int T, int Weff, int h0, int h1,
                                int group) {
   static_assert(D % 2 == 0, "work items of 2 dims");
-  constexpr int MB = IN_KERNEL ? 4 : 8, IPT = 4;
-  auto load2 = [&](const float* src) -> float2 {
-    if constexpr (IN_KERNEL) return load_pair_agent(src);
-    else return *reinterpret_cast<const float2*>(src);
-  };
+  constexpr int MB = 4, IPT = 4;
+  auto load2 = [&](const float* src) -> float2 { return load_pair_agent(src); };
   const int tid = threadIdx.x, NT = blockDim.x, G = p.G;
   const int w_first = range_owner(Pb, T, Weff);
   const int w_last = range_owner(Pb + Tb - 1, T, Weff);
@@ -471,8 +465,107 @@ __device__ void merge_sequence(const AttnParams& p, int b, int Pb, int Tb, int T
       }
     }
   }
-  if (IN_KERNEL && tid == 0)
+  if (tid == 0)
     __hip_atomic_store(p.counters + (int64_t)group * p.B + b, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Heads per workgroup of the separate merge: 128 threads, one pair of dims
+// each, so a workgroup covers 256 / D heads (one head, looped, past D = 256).
+template <int D>
+constexpr int split_merge_heads() { return D >= 256 ? 1 : 256 / D; }
+
+// Body of the separate merge kernel that the whole-row decode kernels launch
+// after themselves on the same stream (so their partial stores are visible):
+// one workgroup of 128 threads per (sequence b = blockIdx.x, heads
+// [split_merge_heads<D>() * blockIdx.y, ...)).  It recomputes the stream-K
+// split of the decode launch (the same tile counts, total T and workgroup
+// count Weff from the same parameters) and, when the sequence spans several
+// workgroups, combines their (m, l, o) partials.  Empty sequences get zeros.
+// A thread owns one pair of dims of one head and issues the loads of up to
+// MB pieces together, so a sequence split over at most MB workgroups costs a
+// single round trip after the lengths; the running maximum is updated once
+// per batch of MB pieces.
+template <int D, int TT>
+__device__ void split_merge(const AttnParams& p) {
+  constexpr int MH = split_merge_heads<D>(), MB = 16, PAIRS = D / 2, NT = 128;
+  static_assert(D % 2 == 0, "work items of 2 dims");
+  const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int h0 = blockIdx.y * MH, h1 = min(p.H, h0 + MH);
+  __shared__ int red[5];
+  int pre = 0, tot = 0;   // tiles before sequence b and in total
+  for (int i = tid; i < p.B; i += NT) {
+    const int Li = seq_len_lane(p, i);
+    const int t = tiles_of<TT>(Li);
+    tot += t;
+    pre += i < b ? t : 0;
+    if (i == b) red[4] = Li;   // the sequence's own length, from the same loads
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    pre += __shfl_xor(pre, o, 64);
+    tot += __shfl_xor(tot, o, 64);
+  }
+  if (lane == 0) {
+    red[wave] = pre;
+    red[2 + wave] = tot;
+  }
+  __syncthreads();
+  const int Pb = red[0] + red[1], T = red[2] + red[3], L = red[4];
+  const int total = (h1 - h0) * PAIRS;
+  auto store = [&](int h, int d, float r0, float r1) {
+    const int64_t off = (int64_t)b * p.out_seq_stride + (int64_t)h * p.out_head_stride + d;
+    if (p.out_f16) {
+      reinterpret_cast<uint16_t*>(p.out)[off] = f2h(r0);
+      reinterpret_cast<uint16_t*>(p.out)[off + 1] = f2h(r1);
+    } else {
+      reinterpret_cast<float*>(p.out)[off] = r0;
+      reinterpret_cast<float*>(p.out)[off + 1] = r1;
+    }
+  };
+  if (L == 0) {
+    for (int e = tid; e < total; e += NT) store(h0 + e / PAIRS, (e % PAIRS) * 2, 0.f, 0.f);
+    return;
+  }
+  const int Tb = tiles_of<TT>(L);
+  const int Weff = max(1, min(p.W, (T + p.min_tiles - 1) / p.min_tiles));
+  const int w_first = range_owner(Pb, T, Weff), w_last = range_owner(Pb + Tb - 1, T, Weff);
+  if (w_first == w_last) return;   // one workgroup wrote the output
+  const int first_slot = (range_start(w_first, T, Weff) == Pb) ? 0 : 1;
+  for (int e = tid; e < total; e += NT) {
+    const int h = h0 + e / PAIRS, d = (e % PAIRS) * 2;
+    float M = -INFINITY, Ls = 0.f, O0 = 0.f, O1 = 0.f;
+    for (int w0 = w_first; w0 <= w_last; w0 += MB) {
+      float2 ml[MB], o[MB];
+#pragma unroll
+      for (int i = 0; i < MB; ++i) {
+        ml[i] = make_float2(-INFINITY, 0.f);
+        o[i] = make_float2(0.f, 0.f);
+        const int w = w0 + i;
+        if (w <= w_last) {   // uniform: the batch's pieces only
+          const int64_t slot = ((int64_t)w * 2 + (w == w_first ? first_slot : 0)) * p.H + h;
+          ml[i] = *reinterpret_cast<const float2*>(p.part_ml + slot * 2);
+          o[i] = *reinterpret_cast<const float2*>(p.part_o + slot * D + d);
+        }
+      }
+      float Mn = M;
+#pragma unroll
+      for (int i = 0; i < MB; ++i) Mn = fmaxf(Mn, ml[i].x);
+      const float a = __builtin_amdgcn_exp2f(M - Mn);   // 0 for the first batch (M = -inf)
+      Ls *= a;
+      O0 *= a;
+      O1 *= a;
+#pragma unroll
+      for (int i = 0; i < MB; ++i) {
+        const float sc = __builtin_amdgcn_exp2f(ml[i].x - Mn);   // 0 past the last piece
+        Ls += sc * ml[i].y;
+        O0 += sc * o[i].x;
+        O1 += sc * o[i].y;
+      }
+      M = Mn;
+    }
+    const float rL = __builtin_amdgcn_rcpf(Ls);
+    store(h, d, O0 * rL, O1 * rL);
+  }
 }
 
 // Tile loader of the general path: chunk c of a tile is 8 bytes; a thread

@@ -733,49 +733,11 @@ __global__ void __launch_bounds__(NKV * WPK * 64) rows_kernel(const AttnParams p
   // launched after this kernel on the same stream.
 }
 
-// Merge of the split sequences, one workgroup per (sequence, MH heads):
-// recomputes the stream-K split of the decode launch (the same tile counts,
-// total T and workgroup count Weff from the same parameters) and, when the
-// sequence spans several workgroups, combines their (m, l, o) partials.
-// Empty sequences get zeros here.  The decode kernel's partial stores are
-// visible because this kernel runs after it on the same stream.
-constexpr int MH = 8;   // heads per merge workgroup
+// Merge of the split sequences (and zeros for empty ones), launched after the
+// decode kernel on the same stream: split_merge in attention_kernel.h.
 template <int D, int TT>
 __global__ void __launch_bounds__(128) merge_kernel(const AttnParams p) {
-  const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int h0 = blockIdx.y * MH, h1 = min(p.H, h0 + MH);
-  __shared__ int red[4];
-  // tiles before sequence b and in total
-  int pre = 0, tot = 0;
-  for (int i = tid; i < p.B; i += blockDim.x) {
-    const int t = tiles_of<TT>(seq_len_lane(p, i));
-    tot += t;
-    pre += i < b ? t : 0;
-  }
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) {
-    pre += __shfl_xor(pre, o, 64);
-    tot += __shfl_xor(tot, o, 64);
-  }
-  if (lane == 0) {
-    red[wave] = pre;
-    red[2 + wave] = tot;
-  }
-  __syncthreads();
-  const int Pb = red[0] + red[1], T = red[2] + red[3];
-  const int L = seq_len_of(p, b);
-  if (L == 0) {
-    for (int e = tid; e < (h1 - h0) * D; e += blockDim.x) {
-      const int64_t o = (int64_t)b * p.out_seq_stride + (int64_t)(h0 + e / D) * p.out_head_stride + e % D;
-      if (p.out_f16) reinterpret_cast<uint16_t*>(p.out)[o] = 0;
-      else reinterpret_cast<float*>(p.out)[o] = 0.0f;
-    }
-    return;
-  }
-  const int Tb = tiles_of<TT>(L);
-  const int Weff = max(1, min(p.W, (T + p.min_tiles - 1) / p.min_tiles));
-  if (range_owner(Pb, T, Weff) == range_owner(Pb + Tb - 1, T, Weff)) return;   // one workgroup wrote it
-  merge_sequence<D, SRC_PAGED, false>(p, b, Pb, Tb, T, Weff, h0, h1, 0);
+  split_merge<D, TT>(p);
 }
 
 // Workgroups one CU holds at once (cached per kernel; 0 if unknown).
@@ -812,6 +774,7 @@ static int launch(AttnParams p, int groups, hipStream_t stream) {
     hipLaunchKernelGGL(kern, dim3(W, groups), dim3(S::THREADS), S::LDS, stream, p);
   if (int rc = check_launch("paged decode")) return rc;
   if (p.B > 0) {
+    constexpr int MH = split_merge_heads<D>();
     hipLaunchKernelGGL((merge_kernel<D, TT>), dim3(p.B, (p.H + MH - 1) / MH), dim3(128), 0, stream, p);
     return check_launch("paged decode merge");
   }
