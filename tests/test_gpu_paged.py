@@ -153,6 +153,25 @@ def test_paged_edge_lengths_eight_heads_per_kv(H, KV, D, paged_kernel):
     assert np.all(got[[0, 13]] == 0.0)
 
 
+_LONG_CASES = {}
+
+
+@pytest.mark.parametrize("H,KV,D,L", [(32, 4, 64, 120000), (16, 2, 128, 100000)])
+def test_paged_one_sequence_over_hundreds_of_workgroups(H, KV, D, L, paged_kernel):
+    """One long sequence beside two short ones: the stream-K split spreads it
+    over every workgroup of the launch (hundreds of partial pieces), so the
+    merge combines it in many batches of pieces, each rescaled to the running
+    maximum of the ones before."""
+    key = (H, KV, D, L)
+    if key not in _LONG_CASES:   # the case and its float64 reference, shared by both kernels
+        case = make_paged_case(seed=L + D, B=3, H=H, KV=KV, D=D, lens=[L, 7, 0])
+        _LONG_CASES[key] = (case, paged_reference(case))
+    case, ref = _LONG_CASES[key]
+    got = _run_batched(case)
+    assert_close(got, ref, what=f"one sequence of {L} tokens, H={H} D={D}")
+    assert np.all(got[2] == 0.0)
+
+
 def test_paged_student_t_long_context():
     """Config-4 shaped heads (64 q / 8 kv, D=128) with heavy-tailed K/V."""
     case = make_paged_case(seed=4, B=2, H=64, KV=8, D=128, len_range=(4000, 9000), dist="t3")
