@@ -758,9 +758,17 @@ __global__ void __launch_bounds__(NKV * WPK * 64) mfma_kernel(const AttnParams p
     TileRegs R;
     read_tile(smem + st * S::STAGE + kvw * SLOT, R);
     lds_barrier();
-    // tile t+2 into this stage, in three parts spread over the rest of the
-    // iteration
-    constexpr int K1 = (S::NOPS + 2) / 3, K2 = (2 * S::NOPS + 2) / 3;
+    // tile t+2 into this stage, in parts spread over the rest of the
+    // iteration: before the QK products, after the combine and after PV.  With
+    // eight KV heads of one wave each (batch 64, 32 q / 8 KV heads, 64 tokens
+    // of 1,104-byte rows) nothing goes before the products and half after
+    // each of the other two points: 55.0 against 55.4 us per launch.  At the
+    // other shapes thirds measured best (at 64 q / 8 KV heads, batch 8,
+    // 32K-128K keys, the late split cost 1-3 us; issuing everything before the
+    // products cost 2-6 us at both).
+    constexpr bool LATE = D == 128 && NKV == 8 && WPK == 1;
+    constexpr int K1 = LATE ? 0 : (S::NOPS + 2) / 3;
+    constexpr int K2 = LATE ? (S::NOPS + 1) / 2 : (2 * S::NOPS + 2) / 3;
     using IC0 = std::integral_constant<int, 0>;
     using IC1 = std::integral_constant<int, K1>;
     using IC2 = std::integral_constant<int, K2>;
