@@ -731,7 +731,10 @@ struct Heads {
   // in fp32, and carries it as an fp16 high part and its fp16 remainder.
   static constexpr int QP = MODE == SRC_CHANNEL ? 8 : 4;
   uint32_t qpr[KD][QP];
-  float qa, qb, m_run, l_run, vmt;
+  // m_run: the weight reference of the lane's head in base-2 logits (the
+  // running max, or a later tile's max more than kRefDrop below it); m_top:
+  // the running max.
+  float qa, qb, m_run, m_top, l_run, vmt;
   float acc[4][2];   // per head: sum w*lo, sum w*(lo + 16 hi), in units of 2^-24
 
   __device__ void setup(int lane, int wave, int h0, int h1, int G, int kv_lo) {
@@ -755,7 +758,7 @@ struct Heads {
   // layout already multiplied by k_scale; zv = k_zero) by the head's power of
   // two and lay out the query pairs of the head's key dwords.
   __device__ void begin(const float (&qv)[8], const float (&zv)[8], uint8_t* wscr) {
-    m_run = -INFINITY;
+    m_run = m_top = -INFINITY;
     l_run = 0.f;
     vmt = 0.f;
 #pragma unroll
@@ -858,12 +861,17 @@ struct Heads {
       s2[i] = tvalid[i] ? s2[i] : -INFINITY;
       tmax = fmaxf(tmax, s2[i]);
     }
-    // ---- online softmax (running max per head; rescale only when it grows)
+    // ---- online softmax (reference per head; rescale only when the tile's
+    // max exceeds it or lies more than kRefDrop below it)
     tmax = red16_max(tmax);
-    if (__builtin_amdgcn_ballot_w64(tmax > m_run)) {
-      const bool grow = tmax > m_run;
-      const float alpha = grow ? __builtin_amdgcn_exp2f(m_run - tmax) : 1.f;   // 0 when growing from -inf
-      const float m_new = grow ? tmax : m_run;
+    const bool grow = tmax > m_run;
+    // down to the tile's max (finite: the head has a valid token here), at
+    // most kRefFloor below the running max
+    const bool drop = !grow && tmax > -INFINITY && tmax < m_run - kRefDrop;
+    if (__builtin_amdgcn_ballot_w64(grow || drop)) {
+      const float m_new = grow ? tmax : drop ? fmaxf(tmax, m_top - kRefFloor) : m_run;
+      const float alpha = grow || drop ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.f;   // 0 when growing from -inf
+      m_top = fmaxf(m_top, tmax);
       l_run *= alpha;
       vmt *= alpha;
 #pragma unroll

@@ -285,11 +285,13 @@ __global__ void __launch_bounds__(NKV * WPK * 64) mfma_kernel(const AttnParams p
   const uint8_t* const qsl = smem + S::QOFF + wave * 1024;
 
   v4i qb[NSET][KB];                    // A operand: limb lx of head set st's head hq, k-set grp
-  float qa[NSET], qs[NSET], mq[NSET], m_run[NSET], l_run[NSET], vmt[NSET];
+  // m_run: the weight reference R of each head (units of u); m_lo = R minus
+  // kRefDrop base-2 units, m_top the running max, tu = kRefDrop in units of u.
+  float qa[NSET], qs[NSET], mq[NSET], m_run[NSET], l_run[NSET], vmt[NSET], m_lo[NSET], m_top[NSET], tu[NSET];
 #pragma unroll
   for (int st = 0; st < NSET; ++st) {
-    qa[st] = qs[st] = mq[st] = 0.f;
-    m_run[st] = -INFINITY;
+    qa[st] = qs[st] = mq[st] = tu[st] = 0.f;
+    m_run[st] = m_lo[st] = m_top[st] = -INFINITY;
     l_run[st] = vmt[st] = 0.f;
   }
   floatx4 acc[CB][4];                  // PV: [block][E.lo, E.hi, O.lo, O.hi]
@@ -305,7 +307,7 @@ __global__ void __launch_bounds__(NKV * WPK * 64) mfma_kernel(const AttnParams p
   // the slot of wave 2 kvw + st; else in the wave's own), scale head hq to
   // 31-bit integers, and cut limb lx.
   auto begin_set = [&](int st) __attribute__((always_inline)) {
-    m_run[st] = -INFINITY;
+    m_run[st] = m_lo[st] = m_top[st] = -INFINITY;
     l_run[st] = 0.f;
     vmt[st] = 0.f;
     const uint8_t* const qs_slot = TS ? smem + S::QOFF + (2 * kvw + st) * 1024 : qsl;
@@ -369,6 +371,7 @@ __global__ void __launch_bounds__(NKV * WPK * 64) mfma_kernel(const AttnParams p
     }
     qs[st] = for_soft_lane(qsum);
     qa[st] = for_soft_lane(__builtin_amdgcn_ldexpf(kC<D>, -sc));
+    tu[st] = for_soft_lane(__builtin_amdgcn_ldexpf(kRefDrop / kC<D>, sc));
   };
   auto begin = [&]() __attribute__((always_inline)) {
 #pragma unroll
@@ -521,14 +524,26 @@ __global__ void __launch_bounds__(NKV * WPK * 64) mfma_kernel(const AttnParams p
 #pragma unroll
       for (int rb = 1; rb < RBW; ++rb) tl = fmaxf(tl, u[st * RBW + rb]);
       alpha[st] = 1.f;
-      if (__builtin_amdgcn_ballot_w64(tl > m_run[st])) {
+      // The reference moves when some score of the tile exceeds it, or when
+      // some head (a 16-lane row) has no score within kRefDrop of it.
+      const uint64_t up = __builtin_amdgcn_ballot_w64(tl > m_run[st]);
+      const uint64_t near = __builtin_amdgcn_ballot_w64(tl >= m_lo[st]);
+      if (up || some_row_empty(near)) {
         const float tmax = head_max(tl);
         const bool grow = tmax > m_run[st];
-        alpha[st] = grow ? __builtin_amdgcn_exp2f((m_run[st] - tmax) * qa[st]) : 1.f;   // 0 from -inf
+        // down to the tile's max (finite: the head has a valid token here), at
+        // most kRefFloor below the running max
+        const bool drop = !grow && tmax > -INFINITY && tmax < m_lo[st];
+        const float R = grow ? tmax : drop ? fmaxf(tmax, m_top[st] - (kRefFloor / kRefDrop) * tu[st]) : m_run[st];
+        alpha[st] = grow || drop ? __builtin_amdgcn_exp2f((m_run[st] - R) * qa[st]) : 1.f;   // 0 from -inf
         l_run[st] *= alpha[st];
         vmt[st] *= alpha[st];
-        m_run[st] = grow ? tmax : m_run[st];
-        mq[st] = m_run[st] * qa[st];
+        m_top[st] = fmaxf(m_top[st], tmax);
+        m_run[st] = R;
+        m_lo[st] = R - tu[st];
+        // mq stays finite for a head that has seen no valid token yet (the
+        // second wave of a token split past a short sequence's end)
+        mq[st] = grow || drop ? R * qa[st] : mq[st];
         grew = true;
       }
     }

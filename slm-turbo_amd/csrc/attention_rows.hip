@@ -336,14 +336,17 @@ __global__ void __launch_bounds__(NKV * WPK * 64) rows_kernel(const AttnParams p
   uint32_t qpr[4][DQ][4];             // [head slot][dword][pair]
   // Scores are kept as u = step * dot + min * sum(q) * 2^-24 (q.K in units of
   // 2^(24 - e), e the query's scale exponent); qa converts them to base-2
-  // logits, so a weight is exp2((u - m_run) * qa) and m_run is the running
-  // max of u.
+  // logits, so a weight is exp2((u - m_run) * qa) and m_run is the weight
+  // reference of the lane's head: the running max of u, or a later tile's max
+  // when that lies more than kRefDrop base-2 units below it (m_lo = m_run -
+  // tu, tu = kRefDrop in units of u; m_top is the running max).
   float qa = 0.f, qb = 0.f, mq = 0.f, m_run = -INFINITY, l_run = 0.f, vmt = 0.f;
+  float m_lo = -INFINITY, m_top = -INFINITY, tu = 0.f;
   float accl[DQ][4], accf[DQ][4];     // [byte k][head]: sum w * lo, sum w * (lo + 16 hi), units of 2^-24
   const int pc = lane & 15, pq = lane >> 4;   // PV: V column (DQ bytes), token group
 
   auto begin = [&](const uint4 w) {
-    m_run = -INFINITY;
+    m_run = m_lo = m_top = -INFINITY;
     l_run = 0.f;
     vmt = 0.f;
 #pragma unroll
@@ -394,6 +397,7 @@ __global__ void __launch_bounds__(NKV * WPK * 64) rows_kernel(const AttnParams p
       }
     }
     qa = __builtin_amdgcn_ldexpf(kC<D>, 24 - ex);
+    tu = __builtin_amdgcn_ldexpf(kRefDrop / kC<D>, ex - 24);
     qb = __builtin_amdgcn_ldexpf(qsum, -24);
   };
 
@@ -480,13 +484,20 @@ __global__ void __launch_bounds__(NKV * WPK * 64) rows_kernel(const AttnParams p
     float tl = s2[0];
 #pragma unroll
     for (int r = 1; r < S::ROUNDS; ++r) tl = fmaxf(tl, s2[r]);
-    // online softmax: the running max per head is only recomputed (and the
-    // sums rescaled) when some score of the tile exceeds it
-    if (__builtin_amdgcn_ballot_w64(tl > m_run)) {
+    // online softmax: the reference per head is only recomputed (and the
+    // sums rescaled) when some score of the tile exceeds it, or when some head
+    // has no score of the tile within kRefDrop of it
+    const uint64_t up = __builtin_amdgcn_ballot_w64(tl > m_run);
+    const uint64_t near = __builtin_amdgcn_ballot_w64(tl >= m_lo);
+    if (up || some_class4_empty(near)) {
       const float tmax = red16_max(tl);
       const bool grow = tmax > m_run;
+      // down to the tile's max (finite: the head has a valid token here), at
+      // most kRefFloor below the running max
+      const bool drop = !grow && tmax > -INFINITY && tmax < m_lo;
+      const float R = grow ? tmax : drop ? fmaxf(tmax, m_top - (kRefFloor / kRefDrop) * tu) : m_run;
       // 0 when growing from -inf
-      const float alpha = grow ? __builtin_amdgcn_exp2f((m_run - tmax) * qa) : 1.f;
+      const float alpha = grow || drop ? __builtin_amdgcn_exp2f((m_run - R) * qa) : 1.f;
       l_run *= alpha;
       vmt *= alpha;
 #pragma unroll
@@ -498,8 +509,10 @@ __global__ void __launch_bounds__(NKV * WPK * 64) rows_kernel(const AttnParams p
           scale_in_place(accf[k][h], ah);
         }
       }
-      m_run = grow ? tmax : m_run;
-      mq = m_run * qa;
+      m_top = fmaxf(m_top, tmax);
+      m_run = R;
+      m_lo = R - tu;
+      mq = grow || drop ? R * qa : mq;
     }
 #pragma unroll
     for (int r = 0; r < S::ROUNDS; ++r) {

@@ -117,6 +117,28 @@ __device__ __forceinline__ float red16_sum(float x) {
   return x;
 }
 
+// Weight reference of the decode softmax (base-2 logits).  A token's P.V
+// weight is fp16(exp2(s - R) * step) against a per-head reference R.  R
+// follows the running max up, and moves down to a tile's max when that max
+// lies more than kRefDrop below R, but never further than kRefFloor below the
+// running max.  Every tile's largest weight then stays within 2^-kRefDrop of
+// its step, so a long tail of tokens far below an early maximum (an attention
+// sink) keeps fp16 precision instead of underflowing to zero, and the fp32
+// sums, rescaled by exp2(R_old - R_new) <= 2^kRefFloor, stay finite.
+constexpr float kRefDrop = 8.0f;
+constexpr float kRefFloor = 64.0f;
+
+// Whether some 16-lane row of a wave ballot (lanes 16 g .. 16 g + 15) is empty.
+__device__ __forceinline__ bool some_row_empty(uint64_t m) {
+  return (m & 0xffffull) == 0 || (m & 0xffff0000ull) == 0 || (m & 0xffff00000000ull) == 0 ||
+         (m & 0xffff000000000000ull) == 0;
+}
+// Whether some lane class (lane & 3) == g of a wave ballot is empty.
+__device__ __forceinline__ bool some_class4_empty(uint64_t m) {
+  constexpr uint64_t c = 0x1111111111111111ull;
+  return (m & c) == 0 || (m & (c << 1)) == 0 || (m & (c << 2)) == 0 || (m & (c << 3)) == 0;
+}
+
 // Full wave (64-lane) reductions with the hardware's fminf/fmaxf semantics:
 // NaN operands are ignored and -0 orders below +0.
 __device__ __forceinline__ float wave_min(float x) {

@@ -184,3 +184,80 @@ def test_per_channel_decode_wide_range_queries(H, KV, D, S, qmode):
                                          t(scale[1]), t(zero[1]), num_kv_heads=KV)
     torch.cuda.synchronize()
     assert_close(out[:, 0].cpu().numpy(), ref, what=f"per-channel H={H} KV={KV} D={D} S={S} q={qmode}")
+
+
+# ------------------------------------------------------------------ long context, dominant token
+SINK_GAPS = (9.0, 12.0, 15.0, 16.5)          # nats by which the sink leads, per query head (h % 4)
+_SINK_CASES: dict = {}                # built once per module run: ~180 MB of cache per shape
+
+
+def _sink_case(H: int, KV: int, D: int, lens=(131071, 32770), seed: int = 41):
+    """Position 0 of every sequence is an attention sink whose score leads the
+    others by SINK_GAPS[h % 4] nats for query head h; the other scores lie
+    within about +-0.3 nats of each other.  The sink's V row is near zero and
+    the tail's V rows carry a per-dimension offset (N(1, 1)), so the output is
+    the tail's weight (L - 1) e^-gap (0.9 % of the softmax mass at 131071
+    tokens and 16.5 nats) times the offset: a decode that drops or
+    mis-weights the tail's small weights misses it.  Built once per shape and
+    shared by the kernels under test, with its float64 reference."""
+    key = (H, KV, D, tuple(lens), seed)
+    if key in _SINK_CASES:
+        return _SINK_CASES[key]
+    g = torch.Generator().manual_seed(seed)
+    bs = 16
+    lens_t = torch.as_tensor(lens, dtype=torch.int64)
+    nblk = (lens_t + bs - 1) // bs
+    total = int(nblk.sum())
+    perm = torch.randperm(total, generator=g)
+    tables = torch.zeros((len(lens), int(nblk.max())), dtype=torch.int32)
+    off = 0
+    for b in range(len(lens)):
+        n = int(nblk[b])
+        tables[b, :n] = perm[off:off + n].to(torch.int32)
+        off += n
+    top = max(SINK_GAPS)
+    t = top / np.sqrt(D)                      # sink K row: score c * t * sqrt(D) = gap for q = c * ones
+    c = torch.tensor([SINK_GAPS[h % 4] / top for h in range(H)])
+    q = (c[None, :, None] * torch.ones((len(lens), H, D))).half()
+    cache = np.zeros((total, bs, KV, D + 8), dtype=np.uint8)
+    for b, L in enumerate(lens):
+        k = torch.randn((L, KV, D), generator=g) * 0.1
+        k[0] = t
+        v = torch.randn((L, KV, D), generator=g) + 1.0
+        v[0] = torch.randn((KV, D), generator=g) * 0.01
+        pos = torch.arange(L)
+        slots = tables[b, pos // bs].to(torch.int64) * bs + pos % bs
+        oq.quantize_store(k.half().numpy(), v.half().numpy(), cache, slots.numpy(), bs)
+        del k, v
+    case = PagedCase(q, cache, tables, lens_t.to(torch.int32), bs, KV)
+    ref = paged_reference(case)
+    _SINK_CASES[key] = (case, ref)
+    return case, ref
+
+
+@pytest.mark.parametrize("H,KV,D", [(64, 8, 128), (32, 8, 128)])
+def test_paged_long_context_sink(H, KV, D, paged_kernel):
+    """131071 and 32770 tokens behind a sink 9 to 16.5 nats ahead, through
+    both whole-row kernels, against the float64 oracle at the 2e-3 / 1e-2 bar."""
+    case, ref = _sink_case(H, KV, D)
+    # the tail carries a visible share of the output in every head
+    assert (np.abs(ref[0]).mean(axis=-1) > 5e-3).all()
+    assert_close(_run_paged(case), ref, what=f"sink H={H} KV={KV} D={D} kernel={paged_kernel}")
+
+
+def test_paged_long_context_sink_per_wave_kernel():
+    """The same through the per-wave kernel (three KV heads: no whole-row shape)."""
+    case, ref = _sink_case(24, 3, 128)
+    assert_close(_run_paged(case), ref, what="sink H=24 KV=3 D=128 per-wave")
+
+
+@pytest.mark.parametrize("qmode", ["peak13", "peak25"])
+def test_paged_long_context_peaked_query(qmode, paged_kernel):
+    """A peaked softmax (q x 13, x 25) over 120000 N(0,1) tokens."""
+    key = ("peaked", qmode)
+    if key not in _SINK_CASES:
+        case = make_paged_case(seed=43, B=1, H=32, KV=8, D=128, lens=[120000])
+        case.q = _shape_q(case.q, qmode, seed=43)
+        _SINK_CASES[key] = (case, paged_reference(case))
+    case, ref = _SINK_CASES[key]
+    assert_close(_run_paged(case), ref, what=f"long peaked q={qmode} kernel={paged_kernel}")
