@@ -41,7 +41,15 @@ the reference's CPU torch path timed beside it; then the reference's op-level
 tables (one JSON line per case):
 per-channel decode (32/4 and 14/2 heads at head_dim 64, 32/8 at 128; S = 512,
 1024, 2048) and causal prefill (32/4 and 14/2 at 64; S = 512, 1024), each
-against fp16 SDPA over the dequantized K/V broadcast to the query heads.
+against fp16 SDPA over the dequantized K/V broadcast to the query heads
+(err_vs_dequantized), the error against fp16 SDPA over the unquantized K/V
+(err_vs_fp16, the quantization's cost) and the KV bytes (fp16 broadcast to
+the query heads against packed).
+
+--per-channel-model instead prints the reference's model-level comparison:
+batch-1 greedy decode of the same random-init 1.1B model, prompt 512, 64 new
+tokens, steady-state tokens/s of the fp16 path and of the per-channel hook with
+rulers fixed at the first decode step and with rulers refreshed every step.
 
 --full-model instead prints the line of the full-model workload: greedy
 decode of a random-init Llama-style 1.1B model (22 layers, hidden 2048, 32 /
@@ -119,6 +127,34 @@ def traffic_file(w: Workload) -> Path:
     return ROOT / "profiles" / f"{w.tag}_traffic.txt"
 
 
+COUNTERS_FILE = ROOT / "profiles" / "paged_decode_valu_counters.txt"
+
+
+def kernel_source_sha() -> str:
+    """sha256 (16 hex digits) of the HIP sources the library is built from
+    (slm-turbo_amd/csrc, every file, in name order).  The counter summaries under
+    profiles/ carry the value of the build they measured, so a bench line can
+    say whether its committed counters describe the kernels it ran."""
+    import hashlib
+
+    h = hashlib.sha256()
+    for f in sorted((ROOT / "slm-turbo_amd" / "csrc").iterdir()):
+        if f.is_file():
+            h.update(f.name.encode())
+            h.update(f.read_bytes())
+    return h.hexdigest()[:16]
+
+
+def profile_stamp(path: Path):
+    """The kernel_source_sha line of a committed profile summary, or None."""
+    if not path.exists():
+        return None
+    for line in path.read_text().splitlines():
+        if line.startswith("kernel_source_sha:"):
+            return line.split(":", 1)[1].strip()
+    return None
+
+
 def parse_args(argv=None):
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -139,6 +175,11 @@ def parse_args(argv=None):
     ap.add_argument("--fm-batch", type=int, default=32)
     ap.add_argument("--fm-prompt", type=int, default=4096)
     ap.add_argument("--fm-new-tokens", type=int, default=128)
+    ap.add_argument("--per-channel-model", action="store_true",
+                    help="the reference's model-level table instead: batch-1 greedy decode of the 1.1B model, "
+                         "fp16 against the per-channel hook with fixed and with refreshed rulers")
+    ap.add_argument("--pc-prompt", type=int, default=512)
+    ap.add_argument("--pc-new-tokens", type=int, default=64)
     ap.add_argument("--calibrate-copy-mb", type=int, default=0,
                     help="also run a plain device copy of this many MB (counter calibration)")
     return ap.parse_args(argv)
@@ -228,7 +269,7 @@ def read_counter(key: str, w: Workload = WORKLOADS["headline"]):
     """Per-launch instruction count `key` (valu_instructions_per_launch or
     mfma_instructions_per_launch, rocprofv3 SQ_INSTS_VALU / SQ_INSTS_MFMA) from
     the committed counter summary, or None."""
-    path = ROOT / "profiles" / "paged_decode_valu_counters.txt"
+    path = COUNTERS_FILE
     if not path.exists():
         return None
     for line in path.read_text().splitlines():
@@ -326,7 +367,10 @@ def per_channel_configs(kd, dev, timeit, cpu_budget_s) -> None:
             "value": round(achieved, 3), "unit": "GB/s", "us_per_call": round(us, 2),
             "higher_is_better": True, "dtype": "int4 codes x fp16 query, fp32 accumulate",
             "data": "synthetic", "config": {"workload": name, "H": H, "KV": KV, "D": D, "S": S},
-            "roofline": {"bound": "hbm", "achieved": round(achieved, 3), "peak": HBM_PEAK_GBS,
+            # a call moves 0.1-0.5 MB (HBM floor below 0.1 µs): its time is the
+            # launch and a few dependent memory round trips, so the binding
+            # limit is latency; achieved/frac are still priced against HBM
+            "roofline": {"bound": "latency", "achieved": round(achieved, 3), "peak": HBM_PEAK_GBS,
                          "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 6), "traffic": None,
                          "algorithmic_bytes": nbytes, "hbm_floor_us": round(nbytes / HBM_PEAK_GBS / 1e3, 4),
                          "note": "time per back-to-back Python call: launch-latency bound"},
@@ -423,6 +467,10 @@ def op_level(args) -> int:
         try:
             ref = sdpa(q, kb, vb, causal)
             line["err_vs_dequantized"] = float((out - ref.float()).abs().max())
+            # the quantization's own cost: against fp16 SDPA over the unquantized K/V
+            G = H // KV
+            ref16 = sdpa(q, k.repeat_interleave(G, dim=0), v.repeat_interleave(G, dim=0), causal)
+            line["err_vs_fp16"] = float((out - ref16.float()).abs().max())
             line["fp16_sdpa_us"] = round(timeit(lambda: sdpa(q, kb, vb, causal), iters), 2)
             line["speedup_vs_fp16_sdpa"] = round(line["fp16_sdpa_us"] / line["kernel_us"], 3)
         except RuntimeError as e:                         # no flash / memory-efficient kernel here
@@ -481,6 +529,43 @@ def full_model(args) -> int:
     return 0
 
 
+def per_channel_model(args) -> int:
+    """One JSON line: the reference's model-level comparison
+    (kernels/benchmark/benchmark.py:240-269, 316-331) on the random-init 1.1B
+    model: steady-state batch-1 greedy decode tokens/s of the fp16 path and of
+    the per-channel hook with fixed and with refreshed rulers."""
+    import torch
+
+    from adapters import hf_llama
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    torch.cuda.set_device(0)
+    r = hf_llama.run_per_channel_benchmark(args.pc_prompt, args.pc_new_tokens, "cuda:0", args.seed)
+    steady = r["new_tokens"] - r["warm"]
+    result = {
+        "metric": "batch-1 greedy decode tokens/s, per-channel 4-bit hook vs fp16 eager",
+        "value": round(r["per_channel_fixed"]["tokens_per_s"], 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": steady,
+        "warmup": r["warm"],
+        "ms_per_step": round(r["per_channel_fixed"]["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16 weights/activations; int4 per-channel KV codes",
+        "data": "synthetic: random-init weights (seed 0), random prompt token ids",
+        "config": {"workload": f"Llama-style 1.1B greedy decode, batch 1, prompt {r['prompt']}, "
+                               f"{r['new_tokens']} new tokens (the first {r['warm']} untimed)",
+                   **{k: r[k] for k in ("prompt", "new_tokens", "layers", "heads", "kv_heads", "head_dim")}},
+        "fp16_eager": {k: round(v, 4) for k, v in r["fp16"].items()},
+        "per_channel_fixed": {k: round(v, 4) for k, v in r["per_channel_fixed"].items()},
+        "per_channel_refresh": {k: round(v, 4) for k, v in r["per_channel_refresh"].items()},
+    }
+    print(json.dumps(result))
+    return 0
+
+
 def main(argv=None) -> int:
     args = parse_args(argv)
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -490,6 +575,8 @@ def main(argv=None) -> int:
         return 2
     if args.full_model:
         return full_model(args)
+    if args.per_channel_model:
+        return per_channel_model(args)
     if args.op_level:
         return op_level(args)
 
@@ -541,40 +628,9 @@ def main(argv=None) -> int:
         _native.check(lib, fn(*argsets[i % sets]))
     torch.cuda.synchronize()
 
-    # Timed region: K steps back to back, events only at its ends (the whole-job
-    # rate).  Then K more steps with an event pair around every launch, for the
-    # kernel's own duration (the events between launches add a few µs of idle
-    # stream time per step, so they stay out of the first measurement).
     K = args.steps
-    t_start, t_end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()                     # single process: the barrier is this sync
-    t_start.record(stream)
-    for i in range(K):
-        fn(*argsets[i % sets])
-    t_end.record(stream)
-    torch.cuda.synchronize()
-    total_ms = t_start.elapsed_time(t_end)
-    # During these K steps the library also times the decode kernel alone
-    # (slmt_kernel_timing: a HIP event pair stamped from the kernel's dispatch on
-    # the launch stream); its duration, without the merge kernel that follows
-    # it, is the roofline's.
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(K)]
-    _native.check(lib, lib.slmt_kernel_timing(1))
-    for i in range(K):
-        ev[i][0].record(stream)
-        fn(*argsets[i % sets])
-        ev[i][1].record(stream)
-    torch.cuda.synchronize()
-    lib.slmt_kernel_timing(0)
-    kbuf = (ctypes.c_float * K)()
-    nk = lib.slmt_kernel_timing_read(kbuf, K)
-    if nk < 0:
-        raise RuntimeError("kernel timing: " + _native.last_error(lib))
-    kernel_us = sorted(kbuf[:nk])
-    launch_us = sorted(a.elapsed_time(b) * 1e3 for a, b in ev)
-
+    ms_per_step, kernel_us, launch_us, kernel_name = time_steps(lib, fn, argsets, K, stream)
     nbytes = algorithmic_bytes(lens, w)
-    ms_per_step = total_ms / K
     value = nbytes / (ms_per_step * 1e-3) / 1e9
     mean_launch = statistics.fmean(launch_us)
     # the dominant kernel's own duration (the whole-row decode); calls that
@@ -604,7 +660,8 @@ def main(argv=None) -> int:
             "total_tokens": int(lens.sum()), "algorithmic_bytes": nbytes,
             "rotated_sets": sets, "out_dtype": "fp32",
         },
-        "roofline": roofline(nbytes, achieved, w),
+        "kernel": kernel_name or "per-wave kernel (attention_kernel)",
+        "roofline": roofline(nbytes, achieved, w, mean_kernel, ms_per_step * 1e3),
         "kernel_us": ({
             "mean": round(mean_kernel, 2),
             "median": round(statistics.median(kernel_us), 2),
@@ -620,6 +677,8 @@ def main(argv=None) -> int:
             "note": "whole call (decode + merge kernels) inside an event pair",
         },
     }
+    if kernel_name.startswith("mfma_kernel"):
+        result["vector_alu_kernel"] = time_vector_alu_kernel(lib, fn, argsets, K, stream, nbytes)
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(lens, tables, qs[0], caches[0], ref_out, args.cpu_seconds, w)
     else:
@@ -629,13 +688,85 @@ def main(argv=None) -> int:
     return 0
 
 
-def roofline(nbytes: int, achieved: float, w: Workload) -> dict:
+def time_steps(lib, fn, argsets, K: int, stream):
+    """K steps back to back with events only at the ends (the whole-job rate),
+    then K more with an event pair around every call while the library times the
+    decode kernel alone (slmt_kernel_timing: a HIP event pair stamped from the
+    kernel's dispatch on the launch stream; its duration, without the merge
+    kernel that follows, is the roofline's).  The per-call events add a few µs
+    of idle stream time per step, so they stay out of the first measurement.
+    Returns (ms per step, sorted kernel µs, sorted per-call µs, kernel name)."""
+    import torch
+
+    from kernels import _native
+
+    sets = len(argsets)
+    t_start, t_end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()                     # single process: the barrier is this sync
+    t_start.record(stream)
+    for i in range(K):
+        fn(*argsets[i % sets])
+    t_end.record(stream)
+    torch.cuda.synchronize()
+    total_ms = t_start.elapsed_time(t_end)
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(K)]
+    _native.check(lib, lib.slmt_kernel_timing(1))
+    for i in range(K):
+        ev[i][0].record(stream)
+        fn(*argsets[i % sets])
+        ev[i][1].record(stream)
+    torch.cuda.synchronize()
+    lib.slmt_kernel_timing(0)
+    kbuf = (ctypes.c_float * K)()
+    nk = lib.slmt_kernel_timing_read(kbuf, K)
+    if nk < 0:
+        raise RuntimeError("kernel timing: " + _native.last_error(lib))
+    name = (lib.slmt_kernel_timing_kernel() or b"").decode() if nk else ""
+    return total_ms / K, sorted(kbuf[:nk]), sorted(a.elapsed_time(b) * 1e3 for a, b in ev), name
+
+
+def time_vector_alu_kernel(lib, fn, argsets, K: int, stream, nbytes: int) -> dict:
+    """The same steps through the vector-ALU whole-row kernel (no matrix cores;
+    SLMT_PAGED_DECODE=valu, which the library reads on every call), timed the
+    same way in this process after the matrix-core kernel's figures."""
+    import torch
+
+    from kernels import _native
+
+    old = os.environ.get("SLMT_PAGED_DECODE")
+    os.environ["SLMT_PAGED_DECODE"] = "valu"
+    try:
+        for i in range(200):
+            _native.check(lib, fn(*argsets[i % len(argsets)]))
+        torch.cuda.synchronize()
+        ms, kus, _, name = time_steps(lib, fn, argsets, K, stream)
+    finally:
+        if old is None:
+            os.environ.pop("SLMT_PAGED_DECODE", None)
+        else:
+            os.environ["SLMT_PAGED_DECODE"] = old
+    mean_k = statistics.fmean(kus) if kus else None
+    return {
+        "kernel": name,
+        "us_per_step": round(ms * 1e3, 2),
+        "value": round(nbytes / (ms * 1e-3) / 1e9, 2),
+        "pct_of_hbm_peak": round(100.0 * nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 2),
+        "kernel_us_mean": round(mean_k, 2) if mean_k else None,
+        "frac": round(nbytes / (mean_k * 1e-6) / 1e9 / HBM_PEAK_GBS, 4) if mean_k else None,
+        "note": "vector-ALU whole-row kernel (SLMT_PAGED_DECODE=valu), same steps and timing as the main line",
+    }
+
+
+def roofline(nbytes: int, achieved: float, w: Workload, kernel_us: float, step_us: float) -> dict:
     """The roofline object: achieved algorithmic GB/s against the HBM peak, the
     counter-measured HBM bytes, and three floors of a launch: HBM (bytes at
     8 TB/s), VALU issue (SQ_INSTS_VALU wave instructions x 4 cycles over 1024
     SIMDs at 2.1 GHz) and matrix cores (SQ_INSTS_MFMA x 16 cycles over 1024
     SIMDs at 2.1 GHz; both MFMA shapes used are 16-cycle instructions).
-    `binding` names the largest floor."""
+    `bound` names the largest floor; achieved/peak/frac stay in HBM GB/s, and
+    `frac_of_binding_floor` is that floor over the kernel's time.  The counter
+    figures come from the committed summaries; `counters` says whether they
+    were measured on the kernel sources this run was built from."""
     hbm_floor = nbytes / (HBM_PEAK_GBS * 1e9) * 1e6
     valu = read_counter("valu_instructions_per_launch", w)
     mfma = read_counter("mfma_instructions_per_launch", w)
@@ -643,19 +774,30 @@ def roofline(nbytes: int, achieved: float, w: Workload) -> dict:
     valu_floor = valu * VALU_CYCLES / SIMDS / clock * 1e6 if valu else None
     mfma_floor = mfma * MFMA_CYCLES / SIMDS / clock * 1e6 if mfma else None
     floors = {"hbm": hbm_floor, "valu": valu_floor or 0.0, "mfma": mfma_floor or 0.0}
+    binding = max(floors, key=floors.get)
+    sha = kernel_source_sha()
     return {
-        "bound": "hbm",
+        "bound": binding,
         "achieved": round(achieved, 2),
         "peak": HBM_PEAK_GBS,
         "unit": "GB/s",
         "frac": round(achieved / HBM_PEAK_GBS, 4),
+        "frac_per_step": round(nbytes / (step_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+        "frac_of_binding_floor": round(floors[binding] / kernel_us, 4),
         "traffic": read_traffic(w),
         "hbm_floor_us": round(hbm_floor, 2),
         "valu_instructions": valu,
         "valu_floor_us": round(valu_floor, 2) if valu_floor else None,
         "mfma_instructions": mfma,
         "mfma_floor_us": round(mfma_floor, 2) if mfma_floor else None,
-        "binding": max(floors, key=floors.get),
+        "binding": binding,
+        "counters": {
+            "kernel_source_sha": sha,
+            "traffic_file": traffic_file(w).name,
+            "traffic_measured_on_this_source": profile_stamp(traffic_file(w)) == sha,
+            "instructions_file": COUNTERS_FILE.name,
+            "instructions_measured_on_this_source": profile_stamp(COUNTERS_FILE) == sha,
+        },
     }
 
 

@@ -230,9 +230,13 @@ int slmt_prefill_per_channel(const void* q, const void* k_packed, const void* k_
  * creates nothing.  slmt_kernel_timing_read waits for the recorded events,
  * writes up to max_n durations in microseconds (call order) to us, forgets
  * all recorded pairs and returns how many it wrote, or -1 on a HIP error.
+ * slmt_kernel_timing_kernel names the kernel of the most recent timed call
+ * (instantiation and unit, e.g. "mfma_kernel<128,8,1> (matrix cores)"; ""
+ * before any), a string owned by the library.
  */
 int slmt_kernel_timing(int enable);
 int slmt_kernel_timing_read(float* us, int max_n);
+const char* slmt_kernel_timing_kernel(void);
 
 #ifdef __cplusplus
 }

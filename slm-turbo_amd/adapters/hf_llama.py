@@ -31,8 +31,16 @@ cache that the vLLM backend uses (the layout of the batch-64 paged decode):
   transformers' ``eager_attention_forward`` (K/V heads repeated to the query
   heads, fp16 scores, softmax in fp32, fp16 probabilities times V), with each
   batched product taking contiguous operands.
-* ``greedy_decode`` runs prefill plus N greedy decode steps in either mode and
-  ``run_decode_benchmark`` times the decode steps of both modes (tokens/s).
+* ``per_channel_attention`` (registered as ``ATTN_PER_CHANNEL``) is the
+  reference's own harness restated for the per-channel kernels: batch 1, one
+  query token, the layer's fp16 K/V from transformers' cache quantized per
+  channel and attended by the per-channel decode, with the rulers either fixed
+  at the first decode step (new tokens appended against them) or refreshed
+  every step (``PerChannelKV``); every other call is the fp16 baseline.
+* ``greedy_decode`` runs prefill plus N greedy decode steps in any mode,
+  ``run_decode_benchmark`` times the decode steps of the batched modes and
+  ``run_per_channel_benchmark`` the reference's batch-1 per-channel modes
+  (tokens/s).
 
 The model is a random-init ``LlamaForCausalLM`` built locally from a
 ``LlamaConfig`` (``llama_1b_config``: 22 layers, hidden 2048, 32 query / 4 KV
@@ -54,6 +62,7 @@ import torch
 
 ATTN_PACKED = "slm_packed_kv"
 ATTN_FP16 = "slm_fp16_eager"
+ATTN_PER_CHANNEL = "slm_per_channel"
 
 # Stand-in for the kernel module (tests replace it); None -> kernels.kv_dequant
 _kernel_module: Any = None
@@ -102,6 +111,7 @@ def register_attention() -> None:
 
     AttentionInterface.register(ATTN_PACKED, packed_kv_attention)
     AttentionInterface.register(ATTN_FP16, fp16_attention)
+    AttentionInterface.register(ATTN_PER_CHANNEL, per_channel_attention)
 
 
 def set_attention(model, name: str) -> None:
@@ -253,6 +263,83 @@ def fp16_attention(module, query, key, value, attention_mask, scaling=None, drop
 
 
 # =============================================================================
+#  per-channel hook (the reference's batch-1 harness)
+# =============================================================================
+class PerChannelKV:
+    """State of the per-channel hook for one generation (reference
+    kernels/benchmark/benchmark.py:196-237; pass it as the forward's
+    ``per_channel_kv=`` keyword).
+
+    ``mode="fixed"``: at a layer's first decode step its whole K/V is
+    quantized per channel (``quantize_kv``) into a code buffer with
+    ``headroom`` free tokens; later steps quantize only the new tokens against
+    those frozen rulers (``quantize_tensor``) into the buffer, which grows by
+    ``headroom`` when full.  ``mode="refresh"``: every step re-quantizes the
+    layer's whole K/V (rulers always fit the data, O(S) work per step).
+    ``layers[i]`` holds layer i's codes, rulers and token count; ``calls``
+    counts the decode kernel calls.
+    """
+
+    def __init__(self, mode: str = "fixed", headroom: int = 256):
+        if mode not in ("fixed", "refresh"):
+            raise ValueError(f"per-channel mode must be 'fixed' or 'refresh', got {mode!r}")
+        self.mode, self.headroom = mode, headroom
+        self.layers: dict = {}
+        self.calls = 0
+
+    def packed(self, layer_idx: int, kf: torch.Tensor, vf: torch.Tensor):
+        """(k_packed, k_scale, k_zero, v_packed, v_scale, v_zero) of layer
+        ``layer_idx`` for the K/V ``kf``/``vf`` [KV, S, D] fp16 of all its
+        tokens so far."""
+        kd = _kd()
+        S = kf.shape[1]
+        if self.mode == "refresh":
+            return kd.quantize_kv(kf, vf)
+        st = self.layers.get(layer_idx)
+        if st is None or S < st["n"]:
+            kp, ks, kz, vp, vs, vz = kd.quantize_kv(kf, vf)
+            KV, _, half = kp.shape
+            kb = torch.zeros((KV, S + self.headroom, half), dtype=torch.uint8, device=kp.device)
+            vb = torch.zeros_like(kb)
+            kb[:, :S] = kp
+            vb[:, :S] = vp
+            st = self.layers[layer_idx] = dict(kb=kb, vb=vb, ks=ks, kz=kz, vs=vs, vz=vz, n=S)
+        elif S > st["n"]:
+            prev = st["n"]
+            if S > st["kb"].shape[1]:
+                grow = lambda b: torch.cat([b, b.new_zeros((b.shape[0], S - b.shape[1] + self.headroom,
+                                                            b.shape[2]))], dim=1)
+                st["kb"], st["vb"] = grow(st["kb"]), grow(st["vb"])
+            kd.quantize_tensor(kf[:, prev:], st["ks"], st["kz"], out=st["kb"][:, prev:S])
+            kd.quantize_tensor(vf[:, prev:], st["vs"], st["vz"], out=st["vb"][:, prev:S])
+            st["n"] = S
+        n = st["n"]
+        return st["kb"][:, :n], st["ks"], st["kz"], st["vb"][:, :n], st["vs"], st["vz"]
+
+
+def per_channel_attention(module, query, key, value, attention_mask, scaling=None, dropout=0.0,
+                          per_channel_kv: Optional[PerChannelKV] = None, **kwargs):
+    """The reference's ``slm_kernel`` attention (benchmark.py:196-237) over the
+    per-channel kernels: for batch 1, one query token and more than one cached
+    token, the layer's K/V (transformers' cache, [1, KV, S, D]) are quantized
+    per channel as ``per_channel_kv`` says and attended by
+    ``kv_dequant_decode_attention``; anything else is the fp16 baseline.
+    query [B, H, T, D] -> ([B, T, H, D], None)."""
+    B, H, T, D = query.shape
+    KV, S = key.shape[1], key.shape[2]
+    if per_channel_kv is None or not (B == 1 and T == 1 and S > 1):
+        return fp16_attention(module, query, key, value, attention_mask, scaling, dropout, **kwargs)
+    _check_scale(scaling, D)
+    kd = _kd()
+    kf = key[0].to(torch.float16).contiguous()
+    vf = value[0].to(torch.float16).contiguous()
+    kp, ks, kz, vp, vs, vz = per_channel_kv.packed(module.layer_idx, kf, vf)
+    out = kd.kv_dequant_decode_attention(query[0].to(torch.float16), kp, ks, kz, vp, vs, vz, num_kv_heads=KV)
+    per_channel_kv.calls += 1
+    return out.to(query.dtype).transpose(0, 1).unsqueeze(0), None     # [1, 1, H, D]
+
+
+# =============================================================================
 #  greedy decode and timing
 # =============================================================================
 class DecodeRunner:
@@ -273,6 +360,7 @@ class DecodeRunner:
         cfg = model.config
         self.model, self.mode = model, mode
         self.graph = None
+        self.per_channel: Optional[PerChannelKV] = None
         self._use_graph = bool(graph)
         if graph and mode != "packed":
             raise ValueError("graph capture serves the packed mode only")
@@ -282,14 +370,21 @@ class DecodeRunner:
             dev = next(model.parameters()).device
             self.cache = PackedKVCache(cfg.num_hidden_layers, batch, max_len, cfg.num_key_value_heads, head_dim,
                                        block_size, dev, seed)
-        elif mode == "fp16":
+        elif mode == "fp16" or mode.startswith("per_channel_"):
             from transformers import DynamicCache
 
-            set_attention(model, ATTN_FP16)
+            if mode == "fp16":
+                set_attention(model, ATTN_FP16)
+            else:
+                if batch != 1:
+                    raise ValueError("the per-channel modes serve batch 1 (the reference's harness)")
+                self.per_channel = PerChannelKV(mode[len("per_channel_"):])
+                set_attention(model, ATTN_PER_CHANNEL)
             self.cache = DynamicCache(config=cfg)
             self.length = 0
         else:
-            raise ValueError(f"mode must be 'packed' or 'fp16', got {mode!r}")
+            raise ValueError(f"mode must be 'packed', 'fp16', 'per_channel_fixed' or 'per_channel_refresh', "
+                             f"got {mode!r}")
 
     @torch.no_grad()
     def __call__(self, ids: torch.Tensor) -> torch.Tensor:
@@ -303,7 +398,9 @@ class DecodeRunner:
         else:
             pos = torch.arange(self.length, self.length + n, device=ids.device).unsqueeze(0).expand(ids.shape[0], n)
             self.length += n
-            out = self.model(ids, position_ids=pos, past_key_values=self.cache, use_cache=True, logits_to_keep=1)
+            extra = {} if self.per_channel is None else {"per_channel_kv": self.per_channel}
+            out = self.model(ids, position_ids=pos, past_key_values=self.cache, use_cache=True, logits_to_keep=1,
+                             **extra)
         return out.logits[:, -1]
 
     def _forward(self, ids):
@@ -427,4 +524,49 @@ def run_decode_benchmark(batch: int = 32, prompt: int = 4096, new_tokens: int = 
     res["first_decode_logits_cosine_min"] = float(torch.nn.functional.cosine_similarity(a[2], b[2], dim=-1).min())
     res["greedy_token_agreement"] = float((a[0] == b[0]).float().mean())
     res["graph_tokens_equal_eager"] = bool(torch.equal(kept["packed"][0], kept["packed_graph"][0]))
+    return res
+
+
+def run_per_channel_benchmark(prompt: int = 512, new_tokens: int = 64, device="cuda:0", seed: int = 0,
+                              repeats: int = 2, warm: int = 6, config=None) -> dict:
+    """The reference's model-level table (benchmark.py:240-269, 316-331) on the
+    1.1B model: batch-1 greedy decode with the fp16 baseline and the two
+    per-channel modes (rulers fixed at the first decode step, or refreshed
+    every step), steady-state tokens/s over the steps after the first
+    ``warm``, each mode ``repeats`` times (the last is kept)."""
+    config = config or llama_1b_config()
+    model = build_model(config, device, seed=seed)
+    g = torch.Generator().manual_seed(seed + 1)
+    ids = torch.randint(0, config.vocab_size, (1, prompt), generator=g).to(device)
+    res: dict = {"batch": 1, "prompt": prompt, "new_tokens": new_tokens, "warm": warm,
+                 "layers": config.num_hidden_layers, "heads": config.num_attention_heads,
+                 "kv_heads": config.num_key_value_heads, "head_dim": config.head_dim}
+    kept = {}
+    for mode in ("fp16", "per_channel_fixed", "per_channel_refresh"):
+        for _ in range(repeats):
+            run = DecodeRunner(model, mode, 1, prompt + new_tokens, seed=seed)
+            with torch.no_grad():
+                logits = [run(ids)]
+                nxt = logits[0].argmax(-1, keepdim=True)
+                times, toks = [], []
+                for _i in range(new_tokens):
+                    torch.cuda.synchronize()
+                    t0 = time.perf_counter()
+                    logits.append(run(nxt))
+                    nxt = logits[-1].argmax(-1, keepdim=True)
+                    torch.cuda.synchronize()
+                    times.append(time.perf_counter() - t0)
+                    toks.append(nxt)
+            steady = times[warm:]
+            kept[mode] = (torch.cat(toks, dim=1), logits[1].float())
+            res[mode] = {"tokens_per_s": len(steady) / sum(steady), "ms_per_step": sum(steady) / len(steady) * 1e3}
+            if run.per_channel is not None:
+                res[mode]["kernel_calls"] = run.per_channel.calls
+            del run, logits
+            torch.cuda.empty_cache()
+    for mode in ("per_channel_fixed", "per_channel_refresh"):
+        res[mode]["speedup_vs_fp16"] = res[mode]["tokens_per_s"] / res["fp16"]["tokens_per_s"]
+        res[mode]["first_decode_logits_cosine"] = float(torch.nn.functional.cosine_similarity(
+            kept["fp16"][1], kept[mode][1], dim=-1).min())
+        res[mode]["greedy_token_agreement"] = float((kept["fp16"][0] == kept[mode][0]).float().mean())
     return res

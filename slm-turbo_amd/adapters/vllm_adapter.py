@@ -52,8 +52,11 @@ except Exception as e:  # pragma: no cover - depends on the environment
     VLLM_IMPORT_ERROR = f"{type(e).__name__}: {e}"
 
 SUPPORTED_HEAD_SIZES = (64, 80, 128)
-# Decode launches served by the kernel in this process (diagnostics).
+# Decode attention served by the kernel in this process (diagnostics): query
+# rows, one per request of a decode step, as the reference counts its
+# per-request calls (adapters/vllm_adapter.py:63,279), and batched launches.
 _KERNEL_CALLS = 0
+_KERNEL_LAUNCHES = 0
 
 
 def packed_kv_cache_shape(num_blocks: int, block_size: int, num_kv_heads: int, head_size: int) -> tuple:
@@ -194,7 +197,7 @@ class PackedKVAttentionMixin:
         """One batched paged decode launch: query row n attends to the first
         seq_lens[n] tokens of block-table row n.  Writes output[:N] (in place
         when the output buffer allows)."""
-        global _KERNEL_CALLS
+        global _KERNEL_CALLS, _KERNEL_LAUNCHES
         kd = self._slm_kernels()
         block_size, num_kv_heads = kv_cache.shape[1], kv_cache.shape[2]
         if seq_lens.dtype != torch.int32:
@@ -208,7 +211,11 @@ class PackedKVAttentionMixin:
                                                  out_dtype=None if out3 is not None else torch.float32)
         if out3 is None:
             self._store_output(output, res, N)
-        _KERNEL_CALLS += 1
+        _KERNEL_CALLS += N
+        _KERNEL_LAUNCHES += 1
+        if not getattr(self, "_slm_logged", False):       # once per layer implementation, as the reference
+            self._slm_logged = True
+            logger.info("slm-turbo 4-bit decode kernel serving inside vLLM (head_size=%d)", self.head_size)
 
 
 # ---------------------------------------------------------------------------
@@ -369,7 +376,8 @@ def backend_status() -> dict:
     """What this process can do: vLLM present, backend registered, kernel
     library loadable (with the error if not)."""
     status = {"vllm_available": VLLM_AVAILABLE, "vllm_error": VLLM_IMPORT_ERROR,
-              "backend_registered": _BACKEND_REGISTERED, "kernel_calls": _KERNEL_CALLS}
+              "backend_registered": _BACKEND_REGISTERED, "kernel_calls": _KERNEL_CALLS,
+              "kernel_launches": _KERNEL_LAUNCHES}
     try:
         from kernels import _native
 

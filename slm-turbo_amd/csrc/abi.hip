@@ -14,14 +14,20 @@ namespace slmt {
 
 namespace {
 thread_local std::string g_error;
+thread_local int g_status = SLMT_OK;
 }
 
 void set_error(const std::string& msg) { g_error = msg; }
-void clear_error() { g_error.clear(); }
+void clear_error() {
+  g_error.clear();
+  g_status = SLMT_OK;
+}
 int fail(int code, const std::string& msg) {
   g_error = msg;
+  g_status = code;
   return code;
 }
+int last_status() { return g_status == SLMT_OK ? SLMT_ERR_INVALID : g_status; }
 int check_launch(const char* what) {
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(SLMT_ERR_HIP, std::string(what) + ": launch failed: " + hipGetErrorString(e));
@@ -81,7 +87,7 @@ int check_contig(const char* phase, const void* q, const void* kp, const void* v
 
 int check_workspace(const char* phase, int B, int H, int KV, int D, const void* ws, int64_t ws_bytes) {
   const int64_t need = attention_workspace_bytes(B, H, KV, D);
-  if (need < 0) return SLMT_ERR_INVALID;
+  if (need < 0) return last_status();
   if (!ws || ws_bytes < need)
     return fail(SLMT_ERR_INVALID, std::string(phase) + ": workspace of " + s(need) + " bytes required, got " + s(ws_bytes));
   return SLMT_OK;
@@ -369,6 +375,8 @@ int slmt_kernel_timing(int enable) {
   clear_error();
   return set_kernel_timing(enable != 0);
 }
+
+const char* slmt_kernel_timing_kernel(void) { return kernel_timing_kernel(); }
 
 int slmt_kernel_timing_read(float* us, int max_n) {
   clear_error();

@@ -20,6 +20,7 @@ struct KernelTiming {
   bool on = false;
   std::vector<std::pair<hipEvent_t, hipEvent_t>> pool;
   int used = 0;
+  const char* last = "";   // kernel of the most recent timed call
 };
 KernelTiming& kernel_timing() {
   static KernelTiming t;
@@ -27,14 +28,21 @@ KernelTiming& kernel_timing() {
 }
 }  // namespace
 
-bool kernel_timing_events(hipEvent_t* start, hipEvent_t* stop) {
+bool kernel_timing_events(hipEvent_t* start, hipEvent_t* stop, const char* kernel) {
   KernelTiming& t = kernel_timing();
   std::lock_guard<std::mutex> lock(t.mu);
   if (!t.on || t.used >= (int)t.pool.size()) return false;
   *start = t.pool[t.used].first;
   *stop = t.pool[t.used].second;
   ++t.used;
+  t.last = kernel;
   return true;
+}
+
+const char* kernel_timing_kernel() {
+  KernelTiming& t = kernel_timing();
+  std::lock_guard<std::mutex> lock(t.mu);
+  return t.last;
 }
 
 int set_kernel_timing(bool enable) {

@@ -732,8 +732,8 @@ struct Heads {
   static constexpr int QP = MODE == SRC_CHANNEL ? 8 : 4;
   uint32_t qpr[KD][QP];
   // m_run: the weight reference of the lane's head in base-2 logits (the
-  // running max, or a later tile's max more than kRefDrop below it); m_top:
-  // the running max.
+  // running max, or kRefDrop / 2 above a later tile's max more than kRefDrop
+  // below it); m_top: the running max.
   float qa, qb, m_run, m_top, l_run, vmt;
   float acc[4][2];   // per head: sum w*lo, sum w*(lo + 16 hi), in units of 2^-24
 
@@ -865,11 +865,11 @@ struct Heads {
     // max exceeds it or lies more than kRefDrop below it)
     tmax = red16_max(tmax);
     const bool grow = tmax > m_run;
-    // down to the tile's max (finite: the head has a valid token here), at
-    // most kRefFloor below the running max
+    // down to half the threshold above the tile's max (finite: the head has
+    // a valid token here), at most kRefFloor below the running max
     const bool drop = !grow && tmax > -INFINITY && tmax < m_run - kRefDrop;
     if (__builtin_amdgcn_ballot_w64(grow || drop)) {
-      const float m_new = grow ? tmax : drop ? fmaxf(tmax, m_top - kRefFloor) : m_run;
+      const float m_new = grow ? tmax : drop ? fmaxf(tmax + 0.5f * kRefDrop, m_top - kRefFloor) : m_run;
       const float alpha = grow || drop ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.f;   // 0 when growing from -inf
       m_top = fmaxf(m_top, tmax);
       l_run *= alpha;

@@ -37,9 +37,13 @@
 // A V byte pair of one token is read with ds_read_u16, two tokens are packed
 // with one v_perm, and each nibble becomes an fp16 subnormal n * 2^-24 (or
 // 16 n * 2^-24) with one AND, which the matrix core multiplies exactly by the
-// weight.  Weights w = fp16(p * step); the softmax sums use the probability
-// each weight stands for, w / step, so the output is an exact weighted mean of
-// the dequantized rows.  The per-token min enters once per token as sum(p * min).
+// weight.  Weights w = fp16(p * step) go into the B columns of the wave's
+// heads; the columns the heads leave free carry each weight's remainder,
+// fp16((p * step - w) * 2^11), so a column pair holds p * step to ~22 bits
+// down to 2^-25 and to within 2^-36 below (a lone fp16 weight loses precision
+// below 2^-14 and vanishes below 2^-25: a long tail behind a dominant token
+// would drop out).  The pair is joined once per segment; the softmax sums use
+// p itself, and the per-token min enters once per token as sum(p * min).
 #include "attention_kernel.h"
 
 #include <hip/hip_ext.h>
@@ -49,6 +53,7 @@
 #include <cstring>
 #include <map>
 #include <mutex>
+#include <string>
 #include <tuple>
 #include <type_traits>
 
@@ -84,7 +89,9 @@ struct Shape {
   static constexpr int TH = TT / 32;            // PV token halves
   static constexpr int STAGE = TT * RSTRIDE;
   static constexpr int QOFF = NS * STAGE;       // one 1 KB query slot per wave
-  static constexpr int WSZ = 4 * TT * 2;        // per-wave weights: 4 heads x TT tokens, fp16
+  // per-wave weights, fp16: 4 heads x TT tokens (or 8 heads x TT / 2 with the
+  // token split), then their remainders in the same layout
+  static constexpr int WSZ = 2 * 4 * TT * 2;
   static constexpr int WOFF = QOFF + WAVES * 1024;
   static constexpr int ZOFF = WOFF + WAVES * WSZ;   // 128 zero bytes (B operand of unused columns)
   static constexpr int MOFF = ZOFF + 128;
@@ -285,13 +292,11 @@ __global__ void __launch_bounds__(NKV * WPK * 64) mfma_kernel(const AttnParams p
   const uint8_t* const qsl = smem + S::QOFF + wave * 1024;
 
   v4i qb[NSET][KB];                    // A operand: limb lx of head set st's head hq, k-set grp
-  // m_run: the weight reference R of each head (units of u); m_lo = R minus
-  // kRefDrop base-2 units, m_top the running max, tu = kRefDrop in units of u.
-  float qa[NSET], qs[NSET], mq[NSET], m_run[NSET], l_run[NSET], vmt[NSET], m_lo[NSET], m_top[NSET], tu[NSET];
+  float qa[NSET], qs[NSET], mq[NSET], m_run[NSET], l_run[NSET], vmt[NSET];
 #pragma unroll
   for (int st = 0; st < NSET; ++st) {
-    qa[st] = qs[st] = mq[st] = tu[st] = 0.f;
-    m_run[st] = m_lo[st] = m_top[st] = -INFINITY;
+    qa[st] = qs[st] = mq[st] = 0.f;
+    m_run[st] = -INFINITY;
     l_run[st] = vmt[st] = 0.f;
   }
   floatx4 acc[CB][4];                  // PV: [block][E.lo, E.hi, O.lo, O.hi]
@@ -307,7 +312,7 @@ __global__ void __launch_bounds__(NKV * WPK * 64) mfma_kernel(const AttnParams p
   // the slot of wave 2 kvw + st; else in the wave's own), scale head hq to
   // 31-bit integers, and cut limb lx.
   auto begin_set = [&](int st) __attribute__((always_inline)) {
-    m_run[st] = m_lo[st] = m_top[st] = -INFINITY;
+    m_run[st] = -INFINITY;
     l_run[st] = 0.f;
     vmt[st] = 0.f;
     const uint8_t* const qs_slot = TS ? smem + S::QOFF + (2 * kvw + st) * 1024 : qsl;
@@ -371,7 +376,6 @@ __global__ void __launch_bounds__(NKV * WPK * 64) mfma_kernel(const AttnParams p
     }
     qs[st] = for_soft_lane(qsum);
     qa[st] = for_soft_lane(__builtin_amdgcn_ldexpf(kC<D>, -sc));
-    tu[st] = for_soft_lane(__builtin_amdgcn_ldexpf(kRefDrop / kC<D>, sc));
   };
   auto begin = [&]() __attribute__((always_inline)) {
 #pragma unroll
@@ -524,26 +528,14 @@ __global__ void __launch_bounds__(NKV * WPK * 64) mfma_kernel(const AttnParams p
 #pragma unroll
       for (int rb = 1; rb < RBW; ++rb) tl = fmaxf(tl, u[st * RBW + rb]);
       alpha[st] = 1.f;
-      // The reference moves when some score of the tile exceeds it, or when
-      // some head (a 16-lane row) has no score within kRefDrop of it.
-      const uint64_t up = __builtin_amdgcn_ballot_w64(tl > m_run[st]);
-      const uint64_t near = __builtin_amdgcn_ballot_w64(tl >= m_lo[st]);
-      if (up || some_row_empty(near)) {
+      if (__builtin_amdgcn_ballot_w64(tl > m_run[st])) {
         const float tmax = head_max(tl);
         const bool grow = tmax > m_run[st];
-        // down to the tile's max (finite: the head has a valid token here), at
-        // most kRefFloor below the running max
-        const bool drop = !grow && tmax > -INFINITY && tmax < m_lo[st];
-        const float R = grow ? tmax : drop ? fmaxf(tmax, m_top[st] - (kRefFloor / kRefDrop) * tu[st]) : m_run[st];
-        alpha[st] = grow || drop ? __builtin_amdgcn_exp2f((m_run[st] - R) * qa[st]) : 1.f;   // 0 from -inf
+        alpha[st] = grow ? __builtin_amdgcn_exp2f((m_run[st] - tmax) * qa[st]) : 1.f;   // 0 from -inf
         l_run[st] *= alpha[st];
         vmt[st] *= alpha[st];
-        m_top[st] = fmaxf(m_top[st], tmax);
-        m_run[st] = R;
-        m_lo[st] = R - tu[st];
-        // mq stays finite for a head that has seen no valid token yet (the
-        // second wave of a token split past a short sequence's end)
-        mq[st] = grow || drop ? R * qa[st] : mq[st];
+        m_run[st] = grow ? tmax : m_run[st];
+        mq[st] = m_run[st] * qa[st];
         grew = true;
       }
     }
@@ -554,7 +546,7 @@ __global__ void __launch_bounds__(NKV * WPK * 64) mfma_kernel(const AttnParams p
 #pragma unroll
         for (int k = 0; k < 4; ++k) acc[c][k] *= ap;
     }
-    uint32_t wv[4];
+    uint32_t wv[4], wr[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int st = r / RBW, rb = r % RBW;
@@ -564,22 +556,22 @@ __global__ void __launch_bounds__(NKV * WPK * 64) mfma_kernel(const AttnParams p
       const float pr = __builtin_amdgcn_exp2f(__builtin_fmaf(u[r], qa[st], -mq[st]));
       const float vstep = h2f((uint16_t)(vr[rb] >> 16));
       const _Float16 wh = (_Float16)(pr * vstep);
-      const uint32_t w = __builtin_bit_cast(uint16_t, wh);
-      // P.V applies w; the sums take the probability it stands for, w / step.
-      // Steps below 2^-10 (fp16 bits below 0x1400; steps are not negative)
-      // keep pr: there the difference moves the output by less than 2^-22 of
-      // the token's weight.
-      const float pp = (int)vr[rb] >= 0x14000000 ? (float)wh * __builtin_amdgcn_rcpf(vstep) : pr;
-      l_run[st] += pp;
-      vmt[st] = __builtin_fmaf(pp, h2f((uint16_t)(vr[rb] & 0xffffu)), vmt[st]);
-      wv[r] = w;
+      // remainder in units of 2^-11: at most half an ulp of a weight below
+      // 65504 (16), so it never overflows; normal down to remainders of 2^-25
+      const float rem = __builtin_fmaf(pr, vstep, -(float)wh);
+      l_run[st] += pr;
+      vmt[st] = __builtin_fmaf(pr, h2f((uint16_t)(vr[rb] & 0xffffu)), vmt[st]);
+      wv[r] = __builtin_bit_cast(uint16_t, wh);
+      wr[r] = __builtin_bit_cast(uint16_t, (_Float16)(rem * 2048.0f));
     }
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int st = r / RBW, rb = r % RBW;
       uint16_t* wh = reinterpret_cast<uint16_t*>(wscr) + (4 * st + grp) * TTW;
       // token 16 rb + col of the wave's tokens: token half rb >> 1, local 16 (rb & 1) + col
-      wh[32 * (rb >> 1) + wpos(16 * (rb & 1) + col)] = (uint16_t)wv[r];
+      const int at = 32 * (rb >> 1) + wpos(16 * (rb & 1) + col);
+      wh[at] = (uint16_t)wv[r];
+      wh[HPW * TTW + at] = (uint16_t)wr[r];   // the remainder column of the same head
     }
   };
 
@@ -589,7 +581,9 @@ __global__ void __launch_bounds__(NKV * WPK * 64) mfma_kernel(const AttnParams p
     half8 bw[THW];
 #pragma unroll
     for (int th = 0; th < THW; ++th) {
-      const uint8_t* src = col < HPW ? wscr + (col * TTW + 32 * th + 8 * grp) * 2 : smem + S::ZOFF + 64 * th + 16 * grp;
+      // columns HPW + h hold head h's remainders (zeros past 2 HPW)
+      const uint8_t* src =
+          col < 2 * HPW ? wscr + (col * TTW + 32 * th + 8 * grp) * 2 : smem + S::ZOFF + 64 * th + 16 * grp;
       bw[th] = *reinterpret_cast<const half8*>(src);
     }
 #pragma unroll
@@ -680,6 +674,16 @@ __global__ void __launch_bounds__(NKV * WPK * 64) mfma_kernel(const AttnParams p
       vt = __builtin_fmaf(vt, f0, f1 * v1);
       mt = M;
     }
+    // join each head's column with its remainder column, HPW lanes up
+#pragma unroll
+    for (int c = 0; c < CB; ++c)
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float lo = HPW == 4 ? dpp_f<DPP_ROW_SHL4>(acc[c][k][r]) : dpp_f<DPP_ROW_ROR8>(acc[c][k][r]);
+          acc[c][k][r] = __builtin_fmaf(lo, 0x1p-11f, acc[c][k][r]);
+        }
     const bool final_out = whole && last_of_seq;
     const float rL = final_out ? __builtin_amdgcn_rcpf(lt) : 1.0f;
 #pragma unroll
@@ -839,6 +843,14 @@ static int blocks_per_cu(const void* kern, int threads, size_t lds) {
   return n;
 }
 
+// Name of an instantiation, for the timing hook.
+template <int D, int NKV, int WPK>
+static const char* kernel_name() {
+  static const std::string n = "mfma_kernel<" + std::to_string(D) + "," + std::to_string(NKV) + "," +
+                               std::to_string(WPK) + "> (matrix cores)";
+  return n.c_str();
+}
+
 template <int D, int NKV, int WPK>
 static int launch(AttnParams p, int groups, hipStream_t stream) {
   using S = Shape<D, NKV, WPK>;
@@ -851,7 +863,7 @@ static int launch(AttnParams p, int groups, hipStream_t stream) {
   p.nthreads = S::THREADS;
   p.heads_per_group = 4 * S::WAVES;
   hipEvent_t ev0, ev1;
-  if (kernel_timing_events(&ev0, &ev1))
+  if (kernel_timing_events(&ev0, &ev1, kernel_name<D, NKV, WPK>()))
     hipExtLaunchKernelGGL(kern, dim3(W, groups), dim3(S::THREADS), S::LDS, stream, ev0, ev1, 0, p);
   else
     hipLaunchKernelGGL(kern, dim3(W, groups), dim3(S::THREADS), S::LDS, stream, p);

@@ -57,6 +57,7 @@
 #include <algorithm>
 #include <map>
 #include <mutex>
+#include <string>
 #include <tuple>
 #include <type_traits>
 
@@ -337,9 +338,9 @@ __global__ void __launch_bounds__(NKV * WPK * 64) rows_kernel(const AttnParams p
   // Scores are kept as u = step * dot + min * sum(q) * 2^-24 (q.K in units of
   // 2^(24 - e), e the query's scale exponent); qa converts them to base-2
   // logits, so a weight is exp2((u - m_run) * qa) and m_run is the weight
-  // reference of the lane's head: the running max of u, or a later tile's max
-  // when that lies more than kRefDrop base-2 units below it (m_lo = m_run -
-  // tu, tu = kRefDrop in units of u; m_top is the running max).
+  // reference of the lane's head: the running max of u, or kRefDrop / 2 above
+  // a later tile's max when that lies more than kRefDrop base-2 units below it
+  // (m_lo = m_run - tu, tu = kRefDrop in units of u; m_top is the running max).
   float qa = 0.f, qb = 0.f, mq = 0.f, m_run = -INFINITY, l_run = 0.f, vmt = 0.f;
   float m_lo = -INFINITY, m_top = -INFINITY, tu = 0.f;
   float accl[DQ][4], accf[DQ][4];     // [byte k][head]: sum w * lo, sum w * (lo + 16 hi), units of 2^-24
@@ -492,10 +493,11 @@ __global__ void __launch_bounds__(NKV * WPK * 64) rows_kernel(const AttnParams p
     if (up || some_class4_empty(near)) {
       const float tmax = red16_max(tl);
       const bool grow = tmax > m_run;
-      // down to the tile's max (finite: the head has a valid token here), at
-      // most kRefFloor below the running max
+      // down to half the threshold above the tile's max (finite: the head
+      // has a valid token here), at most kRefFloor below the running max
       const bool drop = !grow && tmax > -INFINITY && tmax < m_lo;
-      const float R = grow ? tmax : drop ? fmaxf(tmax, m_top - (kRefFloor / kRefDrop) * tu) : m_run;
+      const float R = grow ? tmax : drop ? fmaxf(__builtin_fmaf(0.5f, tu, tmax), m_top - (kRefFloor / kRefDrop) * tu)
+                                         : m_run;
       // 0 when growing from -inf
       const float alpha = grow || drop ? __builtin_amdgcn_exp2f((m_run - R) * qa) : 1.f;
       l_run *= alpha;
@@ -769,6 +771,14 @@ static int blocks_per_cu(const void* kern, int threads, size_t lds) {
   return n;
 }
 
+// Name of an instantiation, for the timing hook.
+template <int D, int NKV, int WPK, int TT>
+static const char* kernel_name() {
+  static const std::string n = "rows_kernel<" + std::to_string(D) + "," + std::to_string(NKV) + "," +
+                               std::to_string(WPK) + "," + std::to_string(TT) + "> (vector ALUs)";
+  return n.c_str();
+}
+
 template <int D, int NKV, int WPK, int TT>
 static int launch(AttnParams p, int groups, hipStream_t stream) {
   using S = Shape<D, NKV, WPK, TT>;
@@ -781,7 +791,7 @@ static int launch(AttnParams p, int groups, hipStream_t stream) {
   p.nthreads = S::THREADS;
   p.heads_per_group = 4 * S::WAVES;
   hipEvent_t ev0, ev1;
-  if (kernel_timing_events(&ev0, &ev1))
+  if (kernel_timing_events(&ev0, &ev1, kernel_name<D, NKV, WPK, TT>()))
     hipExtLaunchKernelGGL(kern, dim3(W, groups), dim3(S::THREADS), S::LDS, stream, ev0, ev1, 0, p);
   else
     hipLaunchKernelGGL(kern, dim3(W, groups), dim3(S::THREADS), S::LDS, stream, p);

@@ -68,7 +68,7 @@ extern "C" int slmt_decode_paged_batched_noalloc(const void* q, int64_t q_seq_st
   if (head_dim != 64 && head_dim != 80 && head_dim != 128)
     return fail(SLMT_ERR_INVALID, "paged decode: head_dim must be 64/80/128, got " + std::to_string(head_dim));
   const int64_t need = attention_workspace_bytes(num_seqs, num_heads, num_kv_heads, head_dim);
-  if (need < 0) return SLMT_ERR_INVALID;
+  if (need < 0) return last_status();   // the sizing's own status and message
   if (need > kScratchBytes)
     return fail(SLMT_ERR_UNSUPPORTED, "paged decode (no-alloc): this call needs " + std::to_string(need) +
                                           " bytes of workspace, above the " + std::to_string(kScratchBytes) +

@@ -16,6 +16,9 @@ namespace slmt {
 void set_error(const std::string& msg);
 void clear_error();
 int fail(int code, const std::string& msg);
+// Status of the calling thread's last fail() since clear_error() (for helpers
+// that report failure through their return value, such as a negative size).
+int last_status();
 int check_launch(const char* what);
 
 // Device properties cached per device (compute-unit count).
@@ -119,19 +122,23 @@ __device__ __forceinline__ float red16_sum(float x) {
 
 // Weight reference of the decode softmax (base-2 logits).  A token's P.V
 // weight is fp16(exp2(s - R) * step) against a per-head reference R.  R
-// follows the running max up, and moves down to a tile's max when that max
-// lies more than kRefDrop below R, but never further than kRefFloor below the
-// running max.  Every tile's largest weight then stays within 2^-kRefDrop of
-// its step, so a long tail of tokens far below an early maximum (an attention
-// sink) keeps fp16 precision instead of underflowing to zero, and the fp32
-// sums, rescaled by exp2(R_old - R_new) <= 2^kRefFloor, stay finite.
-constexpr float kRefDrop = 8.0f;
+// follows the running max up; when a tile's max lies more than kRefDrop below
+// R, R moves down to kRefDrop / 2 above that max, but never further than
+// kRefFloor below the running max.  Every tile's largest weight then stays
+// within 2^-kRefDrop of its step, so a long tail of tokens far below an early
+// maximum (an attention sink) keeps fp16 precision instead of underflowing to
+// zero, and the fp32 sums, rescaled by exp2(R_old - R_new) <= 2^kRefFloor,
+// stay finite.  The half-threshold margin keeps R still while tile maxima
+// wander within +-kRefDrop / 2 of where it moved (heavy-tailed scores would
+// otherwise move it down and up again nearly every tile).
+constexpr float kRefDrop = 10.0f;
 constexpr float kRefFloor = 64.0f;
 
-// Whether some 16-lane row of a wave ballot (lanes 16 g .. 16 g + 15) is empty.
+// Whether some 16-lane row of a wave ballot (lanes 16 g .. 16 g + 15) is
+// empty: a 16-bit field f of m is zero exactly when (m - 1 per field) & ~m
+// has f's top bit set (borrows only reach fields above a zero field).
 __device__ __forceinline__ bool some_row_empty(uint64_t m) {
-  return (m & 0xffffull) == 0 || (m & 0xffff0000ull) == 0 || (m & 0xffff00000000ull) == 0 ||
-         (m & 0xffff000000000000ull) == 0;
+  return ((m - 0x0001000100010001ull) & ~m & 0x8000800080008000ull) != 0;
 }
 // Whether some lane class (lane & 3) == g of a wave ballot is empty.
 __device__ __forceinline__ bool some_class4_empty(uint64_t m) {
@@ -245,7 +252,9 @@ int launch_attention_rows(int D, int nkv, int wpk, int groups, const AttnParams&
 // Event pair for a whole-row decode kernel when slmt_kernel_timing is on: the
 // next free pair of the pool (false when off or full).  The launch passes them
 // to hipExtLaunchKernelGGL, which stamps them from the kernel's own dispatch.
-bool kernel_timing_events(hipEvent_t* start, hipEvent_t* stop);
+// `kernel` (a string with static storage) names the timed kernel.
+bool kernel_timing_events(hipEvent_t* start, hipEvent_t* stop, const char* kernel);
+const char* kernel_timing_kernel();           // slmt_kernel_timing_kernel
 int set_kernel_timing(bool enable);            // slmt_kernel_timing
 int read_kernel_timing(float* us, int max_n);  // slmt_kernel_timing_read
 // Matrix-core variant of the whole-row kernel (attention_mfma.hip): whether it

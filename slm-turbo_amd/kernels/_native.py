@@ -49,6 +49,7 @@ SIGNATURES = {
                                         _i32, _i32, _i32, _i32, _i32, _p_f32, _vp, _i64, _vp]),
     "slmt_kernel_timing": (_i32, [_i32]),
     "slmt_kernel_timing_read": (_i32, [_p_f32, _i32]),
+    "slmt_kernel_timing_kernel": (ctypes.c_char_p, []),
 }
 
 

@@ -14,7 +14,9 @@ dequant-then-attend of the same cache bytes (per-token nib * step + min,
 reference kernels/kv_dequant_kernels.cuh:14-24,666-670,713-722; softmax(q K^T /
 sqrt(D)) V) and against a size-independent property: permuting the physical
 blocks, with the block table permuted to match, leaves every output bit
-unchanged."""
+unchanged.  Every case runs through both whole-row kernels (the matrix-core
+default and the vector-ALU kernel); each workload and its reference are built
+once per module run."""
 from __future__ import annotations
 
 import math
@@ -92,6 +94,22 @@ def reference(q, cache, tables, lens, KV):
     return out
 
 
+_BUILT: dict = {}
+
+
+def workload(name):
+    """(lens, tables, q, cache, reference) of a named full-size workload."""
+    if name not in _BUILT:
+        seed, B, H, KV, D, lo, hi, dist = {
+            "headline": (0, 64, 32, 8, 128, 512, 8192, "normal"),
+            "long-context": (0, 8, 64, 8, 128, 32768, 131072, "t3"),
+            "full-model-attention": (0, 32, 32, 4, 64, 4096, 4224, "normal"),
+        }[name]
+        lens, tables, q, cache = build(seed, B, H, KV, D, lo, hi, dist)
+        _BUILT[name] = (lens, tables, q, cache, reference(q, cache, tables, lens, KV).cpu().numpy())
+    return _BUILT[name]
+
+
 def decode(q, cache, tables, lens, KV):
     kd = _kd()
     out = kd.kv_dequant_decode_paged_batched(q, cache, tables.to(DEV), lens.to(DEV), BS, KV)
@@ -99,20 +117,17 @@ def decode(q, cache, tables, lens, KV):
     return out
 
 
-def test_headline_configuration_full_size():
-    B, H, KV, D = 64, 32, 8, 128
-    lens, tables, q, cache = build(0, B, H, KV, D, 512, 8192, "normal")
-    got = decode(q, cache, tables, lens, KV)
-    ref = reference(q, cache, tables, lens, KV)
-    assert_close(got.cpu().numpy(), ref.cpu().numpy(), what="batch 64, U[512,8192]")
+def test_headline_configuration_full_size(paged_kernel):
+    lens, tables, q, cache, ref = workload("headline")
+    got = decode(q, cache, tables, lens, 8)
+    assert_close(got.cpu().numpy(), ref, what=f"batch 64, U[512,8192], {paged_kernel}")
 
 
-def test_long_context_configuration_full_size():
-    B, H, KV, D = 8, 64, 8, 128
-    lens, tables, q, cache = build(0, B, H, KV, D, 32768, 131072, "t3")
+def test_long_context_configuration_full_size(paged_kernel):
+    B, KV = 8, 8
+    lens, tables, q, cache, ref = workload("long-context")
     got = decode(q, cache, tables, lens, KV)
-    ref = reference(q, cache, tables, lens, KV)
-    assert_close(got.cpu().numpy(), ref.cpu().numpy(), what="batch 8, U[32768,131072], Student-t")
+    assert_close(got.cpu().numpy(), ref, what=f"batch 8, U[32768,131072], Student-t, {paged_kernel}")
 
     # physical block permutation: same logical sequences, every bit unchanged
     nb = cache.shape[0]
@@ -130,12 +145,10 @@ def test_long_context_configuration_full_size():
     assert torch.equal(got, got2)
 
 
-def test_full_model_attention_shape():
+def test_full_model_attention_shape(paged_kernel):
     """The full-model workload's decode: batch 32, 32 query / 4 KV heads,
     head_dim 64, lengths U[4096, 4224] (a 4096-token prompt plus up to 128
     generated tokens)."""
-    B, H, KV, D = 32, 32, 4, 64
-    lens, tables, q, cache = build(0, B, H, KV, D, 4096, 4224, "normal")
-    got = decode(q, cache, tables, lens, KV)
-    ref = reference(q, cache, tables, lens, KV)
-    assert_close(got.cpu().numpy(), ref.cpu().numpy(), what="batch 32, H=32 KV=4 D=64, U[4096,4224]")
+    lens, tables, q, cache, ref = workload("full-model-attention")
+    got = decode(q, cache, tables, lens, 4)
+    assert_close(got.cpu().numpy(), ref, what=f"batch 32, H=32 KV=4 D=64, U[4096,4224], {paged_kernel}")

@@ -127,6 +127,17 @@ def test_paged_block_sizes(bs, D, paged_kernel):
     assert_close(_run_batched(case), paged_reference(case), what=f"bs={bs} D={D}")
 
 
+@pytest.mark.parametrize("bs", [32, 64, 128])
+@pytest.mark.parametrize("H,KV,D", [(32, 8, 128), (64, 8, 128), (16, 2, 128), (32, 4, 64)])
+def test_paged_block_sizes_whole_row_shapes(H, KV, D, bs, paged_kernel):
+    """Blocks of 32-128 tokens at the shapes the whole-row kernels take
+    (8 KV heads x 1 wave, 4 x 2 with the token split, 2 x 2 at head_dim 128,
+    2 x 2 at 64): a wave's staged rows then span several rows of one block,
+    and a 64-token tile covers part of a block instead of four of them."""
+    case = make_paged_case(seed=bs + H, B=4, H=H, KV=KV, D=D, block_size=bs, len_range=(1, 1500))
+    assert_close(_run_batched(case), paged_reference(case), what=f"bs={bs} H={H} KV={KV} D={D}")
+
+
 @pytest.mark.parametrize("D", [64, 128])
 def test_paged_edge_lengths_and_formats(D, paged_kernel):
     """Lengths 0, 1, 15, 16, 17 and a long one; int64 tables; fp16 output."""

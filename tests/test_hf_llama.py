@@ -329,3 +329,140 @@ def test_full_depth_decode_kernel_matches_torch_decode(monkeypatch):
         c = cos(hip[i], ref[i])
         print(f"step {i}: cosine HIP vs torch decode {c:.6f}")
         assert c > 0.999, f"step {i}: cosine {c}"
+
+
+# ---------------------------------------------------------------- per-channel hook (batch 1)
+class _OraclePerChannel:
+    """CPU stand-in for the per-channel entry points: the oracle's quantizer
+    (fp16 round-after-every-op, benchmark.py:26-74) and float64 decode."""
+
+    def __init__(self):
+        self.decode_calls = 0
+
+    def quantize_kv(self, k, v):
+        return tuple(torch.from_numpy(np.ascontiguousarray(a)) for a in oq.quantize_kv(k.numpy(), v.numpy()))
+
+    def quantize_tensor(self, x, scale, zero_point, bits=4, out=None):
+        r = torch.from_numpy(oq.quantize_tensor(x.numpy(), scale.numpy(), zero_point.numpy()))
+        if out is None:
+            return r
+        out.copy_(r)
+        return out
+
+    def kv_dequant_decode_attention(self, q, kp, ks, kz, vp, vs, vz, num_kv_heads=None):
+        self.decode_calls += 1
+        r = oa.decode_per_channel(q.numpy(), kp.numpy(), ks.numpy(), kz.numpy(), vp.numpy(), vs.numpy(),
+                                  vz.numpy())
+        return torch.from_numpy(r).float()
+
+
+def _per_channel_steps(dev, mode, H=8, KV=2, D=64, S0=20, steps=4, headroom=2, seed=3):
+    """Drive per_channel_attention for decode steps over a growing fp16 K/V
+    (S0, S0 + 1, ...): yields (S, got [1,1,H,D], k [KV,S,D], v, q [H,1,D], state)."""
+    g = torch.Generator().manual_seed(seed)
+    st = hl.PerChannelKV(mode, headroom=headroom)
+    K = (torch.randn((1, KV, S0 + steps, D), generator=g) * 1.5).half()
+    V = torch.randn((1, KV, S0 + steps, D), generator=g).half()
+    for i in range(steps):
+        S = S0 + i
+        q = torch.randn((1, H, 1, D), generator=g).half()
+        o, w = hl.per_channel_attention(SimpleNamespace(layer_idx=0), q.to(dev), K[:, :, :S].to(dev),
+                                        V[:, :, :S].to(dev), None, scaling=D ** -0.5, per_channel_kv=st)
+        assert w is None and o.shape == (1, 1, H, D)
+        yield S, o.float().cpu(), K[0, :, :S], V[0, :, :S], q[0], st
+
+
+def _check_per_channel(dev, mode, **kw):
+    first = None
+    for S, got, k, v, q, st in _per_channel_steps(dev, mode, **kw):
+        kn, vn = k.numpy(), v.numpy()
+        if mode == "refresh" or first is None:
+            ks, kz = oq.compute_scale_zero(kn)
+            vs, vz = oq.compute_scale_zero(vn)
+            first = first or (ks, kz, vs, vz)
+        else:
+            ks, kz, vs, vz = first                  # rulers frozen at the first decode step
+        kp, vp = oq.quantize_tensor(kn, ks, kz), oq.quantize_tensor(vn, vs, vz)
+        if mode == "fixed":
+            lay = st.layers[0]
+            assert lay["n"] == S
+            assert np.array_equal(lay["kb"][:, :S].cpu().numpy(), kp), f"K codes, {S} tokens"
+            assert np.array_equal(lay["vb"][:, :S].cpu().numpy(), vp), f"V codes, {S} tokens"
+            assert np.array_equal(lay["ks"].cpu().numpy(), ks) and np.array_equal(lay["vz"].cpu().numpy(), vz)
+        ref = oa.decode_per_channel(q.numpy(), kp, ks, kz, vp, vs, vz)          # [H, 1, D]
+        # the hook returns the model's dtype (fp16): its rounding is inside rel 1e-2
+        assert_close(got[0, 0].numpy(), ref[:, 0], what=f"per-channel {mode}, {S} tokens")
+    assert st.calls == kw.get("steps", 4)
+
+
+@pytest.mark.parametrize("mode", ["fixed", "refresh"])
+def test_per_channel_hook_matches_reference_harness(mode, monkeypatch):
+    """Rulers frozen at the first decode step with each new token quantized
+    against them (the buffer growing past its headroom), or re-derived every
+    step: codes bit-exact with the reference quantizer, outputs within the bar."""
+    monkeypatch.setattr(hl, "_kernel_module", _OraclePerChannel())
+    _check_per_channel("cpu", mode)
+
+
+def test_per_channel_hook_routes_other_calls_to_fp16(monkeypatch):
+    k = _OraclePerChannel()
+    monkeypatch.setattr(hl, "_kernel_module", k)
+    st = hl.PerChannelKV("fixed")
+    g = torch.Generator().manual_seed(0)
+    q, kk, vv = (torch.randn(s, generator=g) for s in ((2, 4, 1, 64), (2, 2, 9, 64), (2, 2, 9, 64)))
+    hl.per_channel_attention(SimpleNamespace(layer_idx=0), q, kk, vv, None, per_channel_kv=st)   # batch 2
+    hl.per_channel_attention(SimpleNamespace(layer_idx=0), q[:1].expand(1, 4, 9, 64).contiguous(),
+                             kk[:1], vv[:1], None, per_channel_kv=st)                         # prefill
+    assert k.decode_calls == 0 and st.calls == 0
+    with pytest.raises(ValueError, match="mode"):
+        hl.PerChannelKV("int8")
+
+
+def test_tiny_model_per_channel_modes(monkeypatch):
+    """Batch-1 greedy decode of a tiny model in both per-channel modes: one
+    decode call per layer and step, logits close to the fp16 path."""
+    k = _OraclePerChannel()
+    monkeypatch.setattr(hl, "_kernel_module", k)
+    model = hl.build_model(_tiny_config(), "cpu", dtype=torch.float32, seed=1)
+    ids = torch.randint(0, 97, (1, 30), generator=torch.Generator().manual_seed(2))
+    _, ref, _, _ = hl.greedy_decode(model, ids, 5, "fp16")
+    for mode in ("per_channel_fixed", "per_channel_refresh"):
+        before = k.decode_calls
+        toks, logits, _, _ = hl.greedy_decode(model, ids, 5, mode)
+        assert toks.shape == (1, 5) and torch.equal(logits[0], ref[0])
+        assert k.decode_calls - before == 2 * 5
+        cos = torch.nn.functional.cosine_similarity(ref[1].double(), logits[1].double(), dim=-1)
+        assert float(cos.min()) > 0.95, (mode, float(cos.min()))
+    with pytest.raises(ValueError, match="batch 1"):
+        hl.DecodeRunner(model, "per_channel_fixed", 2, 40)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("mode", ["fixed", "refresh"])
+@pytest.mark.parametrize("H,KV,D", [(32, 4, 64), (12, 2, 128)])
+def test_per_channel_hook_on_the_gpu(mode, H, KV, D):
+    """The same steps through the HIP quantizers and per-channel decode."""
+    _check_per_channel("cuda:0", mode, H=H, KV=KV, D=D, S0=300, steps=4, headroom=2)
+
+
+@pytest.mark.gpu
+def test_per_channel_model_modes_on_the_gpu():
+    """Two layers of the 1.1B shape at batch 1: both per-channel modes decode
+    through the HIP kernels, one decode call per layer and step, and their
+    first-step logits match the fp16 path's in direction."""
+    cfg = hl.llama_1b_config(num_hidden_layers=2)
+    model = hl.build_model(cfg, "cuda:0", seed=3)
+    ids = torch.randint(0, cfg.vocab_size, (1, 200), generator=torch.Generator().manual_seed(4)).to("cuda:0")
+    _, ref, _, _ = hl.greedy_decode(model, ids, 4, "fp16")
+    for mode in ("per_channel_fixed", "per_channel_refresh"):
+        run = hl.DecodeRunner(model, mode, 1, 204)
+        logits = [run(ids)]
+        nxt = logits[0].argmax(-1, keepdim=True)
+        for _ in range(4):
+            logits.append(run(nxt))
+            nxt = logits[-1].argmax(-1, keepdim=True)
+        assert run.per_channel.calls == 2 * 4
+        assert torch.equal(logits[0], ref[0])
+        cos = float(torch.nn.functional.cosine_similarity(ref[1].double(), logits[1].double(), dim=-1).min())
+        print(f"{mode}: first decode step cosine vs fp16 {cos:.5f}")
+        assert cos > 0.95

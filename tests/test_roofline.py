@@ -110,6 +110,27 @@ def test_benchmark_workloads_have_traffic_summaries(name):
     assert traffic is not None and 1.0 <= traffic / alg < TRAFFIC_BOUND[name]
 
 
+@pytest.mark.parametrize("name", ["headline", "long-context", "full-model-attention"])
+def test_benchmark_roofline_bound_is_the_largest_floor(name):
+    """bench.py's roofline object names the largest of its three floors as the
+    bound and says whether its committed counters match the kernel sources."""
+    import bench
+
+    w = bench.WORKLOADS[name]
+    g = torch.Generator().manual_seed(0)
+    lens = torch.randint(w.lo, w.hi + 1, (w.B,), generator=g)
+    alg = bench.algorithmic_bytes(lens, w)
+    r = bench.roofline(alg, 5000.0, w, kernel_us=60.0, step_us=64.0)
+    floors = {"hbm": r["hbm_floor_us"], "valu": r["valu_floor_us"] or 0.0, "mfma": r["mfma_floor_us"] or 0.0}
+    assert r["bound"] == r["binding"] == max(floors, key=floors.get)
+    assert r["frac"] == pytest.approx(5000.0 / 8000.0)
+    assert r["frac_per_step"] == pytest.approx(alg / 64e-6 / 8e12, rel=1e-3)
+    assert r["frac_of_binding_floor"] == pytest.approx(floors[r["bound"]] / 60.0, rel=1e-3)
+    sha = r["counters"]["kernel_source_sha"]
+    assert len(sha) == 16 and int(sha, 16) >= 0 and sha == bench.kernel_source_sha()
+    assert isinstance(r["counters"]["traffic_measured_on_this_source"], bool)
+
+
 def test_decode_attention_intensity_is_below_the_ridge():
     """4-bit paged decode at G = 4 is memory bound on MI355X by the flop roof
     (~15 flop/B against a ~19.7 flop/B ridge)."""

@@ -112,6 +112,29 @@ def test_decode_is_one_batched_launch_per_layer():
     assert torch.all(out == 0.5)
 
 
+def test_decode_counts_requests_and_logs_once(caplog):
+    """The reference's diagnostics (adapters/vllm_adapter.py:63,279-283): a
+    counter of decode requests served and one "serving inside vLLM" log line
+    per layer implementation; launches are counted beside it."""
+    import logging
+
+    k = _RecordingKernels()
+    impl = _impl(H=8, D=64, KV=2, kernels=k)
+    N = 4
+    q = torch.randn(N, 8, 64).half()
+    cache = torch.zeros(9, 16, 2, 72, dtype=torch.uint8)
+    meta = _meta([3, 40, 5, 17], torch.zeros((N, 3), dtype=torch.int32))
+    before = va.backend_status()
+    with caplog.at_level(logging.INFO, logger="slm_turbo.vllm_adapter"):
+        for _ in range(3):
+            impl.forward(None, q, q, q, cache, meta, torch.zeros(N, 8 * 64, dtype=torch.float16))
+    after = va.backend_status()
+    assert after["kernel_calls"] - before["kernel_calls"] == 3 * N
+    assert after["kernel_launches"] - before["kernel_launches"] == 3
+    lines = [r.getMessage() for r in caplog.records if "serving inside vLLM" in r.getMessage()]
+    assert lines == ["slm-turbo 4-bit decode kernel serving inside vLLM (head_size=64)"]
+
+
 def test_decode_only_the_actual_tokens():
     k = _RecordingKernels()
     impl = _impl(kernels=k)

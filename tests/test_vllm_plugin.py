@@ -201,7 +201,7 @@ def test_pyproject_maps_the_reference_import_names():
     assert set(st["packages"]) == {"adapters", "kernels"}
     for mod in st["py-modules"]:
         assert (src / f"{mod}.py").is_file(), mod
-    assert st["package-data"]["kernels"] == ["libslmturbo_hip.so"]
+    assert st["package-data"]["kernels"] == ["libslmturbo_hip.so", "_slmt_fast*.so"]
     eps = cfg["project"]["entry-points"]["vllm.general_plugins"]
     assert eps == {"slm-turbo": "adapters.vllm_adapter:register_plugin"}
 

@@ -6,7 +6,10 @@ second call runs on the static scratch the first call left behind.  Shapes
 cover the whole-row kernel (no arrival counters) and the per-wave fallback,
 whose last-arriver merges count pieces in the scratch.  Outputs must be
 bit-identical to the workspace entry point's and within 2e-3 / 1e-2 of the
-float64 oracle.  A request whose workspace exceeds the scratch is refused.
+float64 oracle.  Invalid arguments and unsupported sizes fail with the
+workspace entry point's status and message; a request whose workspace would
+exceed the scratch fails with SLMT_ERR_UNSUPPORTED, which on a 256-CU MI355X
+no supported head layout reaches (the scratch holds the largest workspace).
 """
 import ctypes
 
@@ -75,3 +78,28 @@ def test_noalloc_scratch_holds_every_workspace():
                     worst = max(worst, need)
     print(f"largest workspace: {worst} bytes", flush=True)
     assert worst <= 16 * 1024 * 1024
+
+
+def _noalloc_status(lib, B, H, KV, D):
+    """Status and message of a no-alloc call that fails its checks before any
+    pointer is used (null pointers everywhere)."""
+    null = ctypes.c_void_p(0)
+    rc = lib.slmt_decode_paged_batched_noalloc(null, H * D, D, null, 1, 16, null, 32, 1, null, 1, B, H, KV, D,
+                                               null, _native.OUT_F32, H * D, D, null)
+    return rc, _native.last_error(lib)
+
+
+def test_noalloc_reports_the_sizing_status():
+    """Bad arguments give SLMT_ERR_INVALID; more than 2^20 (sequence, head group)
+    pairs give SLMT_ERR_UNSUPPORTED, the same status and message as the
+    workspace entry point's sizing."""
+    lib = _native.load()
+    rc, msg = _noalloc_status(lib, 4, 30, 8, 128)                   # 30 heads over 8 KV heads
+    assert rc == _native.ERR_INVALID and "divisible" in msg
+    rc, msg = _noalloc_status(lib, 4, 32, 8, 96)
+    assert rc == _native.ERR_INVALID and "head_dim" in msg
+    B = (1 << 20) + 1
+    assert lib.slmt_attention_workspace_bytes(B, 32, 8, 128) == -1
+    ws_msg = _native.last_error(lib)
+    rc, msg = _noalloc_status(lib, B, 32, 8, 128)
+    assert rc == _native.ERR_UNSUPPORTED and msg == ws_msg and "2^20" in msg
