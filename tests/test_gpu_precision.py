@@ -68,7 +68,7 @@ def _run_paged(case: PagedCase, out_dtype=torch.float32):
 def test_paged_wide_range_queries(H, KV, D, qmode, dist, paged_kernel):
     case = make_paged_case(seed=3 * H + D, B=3, H=H, KV=KV, D=D, len_range=(200, 1500), dist=dist)
     case.q = _shape_q(case.q, qmode, seed=D + H)
-    assert_close(_run_paged(case), paged_reference(case), what=f"H={H} KV={KV} D={D} q={qmode} kv={dist}")
+    assert_close(_run_paged(case), paged_reference(case), what=f"H={H} KV={KV} D={D} q={qmode} kv={dist} {paged_kernel}")
 
 
 def _extreme_kv(g, L, KV, D):
@@ -101,7 +101,7 @@ def test_paged_extreme_rulers(H, KV, D, qmode, paged_kernel):
         case.q = _shape_q(case.q, qmode, seed=D)
     ref = paged_reference(case)
     assert np.isfinite(ref).all()
-    assert_close(_run_paged(case), ref, what=f"extreme rulers H={H} KV={KV} D={D} q={qmode}")
+    assert_close(_run_paged(case), ref, what=f"extreme rulers H={H} KV={KV} D={D} q={qmode} {paged_kernel}")
 
 
 @pytest.mark.parametrize("H,KV,D", [(32, 8, 128), (32, 4, 64), (64, 8, 128), (8, 8, 80)])
@@ -120,7 +120,7 @@ def test_paged_stale_slots_past_the_end(H, KV, D, paged_kernel):
     case.kv_cache = dirty
     got = _run_paged(case)
     assert np.isfinite(got).all(), "stale slots leaked into the output"
-    assert_close(got, ref, what=f"stale slots H={H} KV={KV} D={D}")
+    assert_close(got, ref, what=f"stale slots H={H} KV={KV} D={D} {paged_kernel}")
 
 
 @pytest.mark.parametrize("H,KV,D", [(32, 8, 128), (32, 4, 64)])
@@ -129,7 +129,7 @@ def test_paged_fp16_output_at_the_bar(H, KV, D, paged_kernel):
     case = make_paged_case(seed=29, B=4, H=H, KV=KV, D=D, len_range=(1, 2500), dist="t3")
     case.q = _shape_q(case.q, "peak13", seed=3)
     assert_close(_run_paged(case, out_dtype=torch.float16), paged_reference(case),
-                 what=f"fp16 out H={H} KV={KV} D={D}")
+                 what=f"fp16 out H={H} KV={KV} D={D} {paged_kernel}")
 
 
 # ------------------------------------------------------------------ contiguous layouts
