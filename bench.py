@@ -561,6 +561,10 @@ def per_channel_model(args) -> int:
         "fp16_eager": {k: round(v, 4) for k, v in r["fp16"].items()},
         "per_channel_fixed": {k: round(v, 4) for k, v in r["per_channel_fixed"].items()},
         "per_channel_refresh": {k: round(v, 4) for k, v in r["per_channel_refresh"].items()},
+        "note": "the logits cosine and token agreement against fp16 measure the per-channel 4-bit "
+                "quantization of the cache; random-init weights give near-flat logits, so greedy tokens "
+                "part at the first step. The hook's kernel output is checked against the float64 oracle "
+                "in tests/test_hf_llama.py",
     }
     print(json.dumps(result))
     return 0
