@@ -146,14 +146,15 @@ __global__ void __launch_bounds__(256 * HP) __attribute__((amdgpu_waves_per_eu(D
   const int vwv = (tid >> 6) & 3;
   const int vk = (lane & 15) + 16 * (vwv & 1), vb = 4 * (vwv >> 1) + (lane >> 4);
   auto zround = [&](int d) { return quant ? fminf(fmaxf(__builtin_rintf(hf(p.vz[(int64_t)kv * D + d])), 0.f), 15.f) : 0.f; };
-  half2v vzc[GG::VW][8];
+  // (1024 + zero) of dims 2b and 2b + 1 of the thread's 8, one register per pair;
+  // the packed subtractions below take one half of it for both lanes (op_sel)
+  half2v vzc[GG::VW][4];
 #pragma unroll
   for (int r = 0; r < GG::VW; ++r)
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const _Float16 z = (_Float16)(1024.0f + zround(8 * (vb + 8 * r) + i));
-      vzc[r][i][0] = z;
-      vzc[r][i][1] = z;
+    for (int b = 0; b < 4; ++b) {
+      vzc[r][b][0] = (_Float16)(1024.0f + zround(8 * (vb + 8 * r) + 2 * b));
+      vzc[r][b][1] = (_Float16)(1024.0f + zround(8 * (vb + 8 * r) + 2 * b + 1));
     }
   const uint8_t* kbase = p.kp + (int64_t)kv * p.S * (D / 2);
   const uint8_t* vbase = p.vp + (int64_t)kv * p.S * (D / 2);
@@ -218,8 +219,10 @@ __global__ void __launch_bounds__(256 * HP) __attribute__((amdgpu_waves_per_eu(D
       for (int b = 0; b < 4; ++b) {
         const int d = 8 * (vb + 8 * r) + 2 * b;  // dims d (low nibbles) and d + 1 (high nibbles)
         const uint32_t sel = 0x0C000C00u | ((4u + b) << 16) | (uint32_t)b;
-        const half2v e = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(lo1, lo0, sel) | 0x64006400u) - vzc[r][2 * b];
-        const half2v o = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(hi1, hi0, sel) | 0x64006400u) - vzc[r][2 * b + 1];
+        const half2v ze = __builtin_shufflevector(vzc[r][b], vzc[r][b], 0, 0);
+        const half2v zo = __builtin_shufflevector(vzc[r][b], vzc[r][b], 1, 1);
+        const half2v e = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(lo1, lo0, sel) | 0x64006400u) - ze;
+        const half2v o = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(hi1, hi0, sel) | 0x64006400u) - zo;
         *reinterpret_cast<uint32_t*>(Vs + d * GG::VROW + 4 * vk) = __builtin_bit_cast(uint32_t, e);
         *reinterpret_cast<uint32_t*>(Vs + (d + 1) * GG::VROW + 4 * vk) = __builtin_bit_cast(uint32_t, o);
       }
@@ -234,7 +237,12 @@ __global__ void __launch_bounds__(256 * HP) __attribute__((amdgpu_waves_per_eu(D
   floatx4 ol = floatx4{0.f, 0.f, 0.f, 0.f};
   const half8 ones = half8{(_Float16)1.0f, (_Float16)1.0f, (_Float16)1.0f, (_Float16)1.0f,
                            (_Float16)1.0f, (_Float16)1.0f, (_Float16)1.0f, (_Float16)1.0f};
-  float m_run = -INFINITY;
+  // The products of S^T accumulate onto -m, m = the column's running maximum
+  // (0 before the first tile), so the scores come out of the matrix cores as
+  // base-2 logits relative to it and need no subtraction per score.  The C
+  // operand is this persistent register block, rewritten only when the maximum
+  // moves; it also is the running maximum's only copy.
+  floatx4 cinit = floatx4{0.f, 0.f, 0.f, 0.f};
 
   using S0 = std::integral_constant<int, 0>;
   using S1 = std::integral_constant<int, 1>;
@@ -263,9 +271,10 @@ __global__ void __launch_bounds__(256 * HP) __attribute__((amdgpu_waves_per_eu(D
     floatx4 s[4];
 #pragma unroll
     for (int n = 0; n < 4; ++n) {
-      s[n] = floatx4{0.f, 0.f, 0.f, 0.f};
+      s[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[n][0], qh[0], cinit, 0, 0, 0);
+      s[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[n][0], ql[0], s[n], 0, 0, 0);
 #pragma unroll
-      for (int j = 0; j < D / 32; ++j) {
+      for (int j = 1; j < D / 32; ++j) {
         s[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[n][j], qh[j], s[n], 0, 0, 0);
         s[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[n][j], ql[j], s[n], 0, 0, 0);
       }
@@ -306,32 +315,40 @@ __global__ void __launch_bounds__(256 * HP) __attribute__((amdgpu_waves_per_eu(D
           tmax = fmaxf(tmax, v);
         }
     }
-    {
+    // The reference maximum moves only when some column's maximum exceeds it by
+    // more than 2^8 (base-2 logits): the weights then stay below 256, well inside
+    // fp16, and the running sums are rescaled rarely (alpha = 0 from the initial
+    // -inf, 1 where a column's maximum did not grow).  Key 0 is visible to every
+    // row, so the first tile sets a finite maximum.  The test runs on the lane's
+    // own 16 scores (some lane exceeds iff some column does); the column maximum
+    // across the four lane groups is formed only when it fires.  s holds
+    // logit - off, and off = m_run once m_run is finite.
+    const float off = -cinit[0];
+    const float m_run = t == 0 ? -INFINITY : off;
+    if (__builtin_amdgcn_ballot_w64(tmax > (t == 0 ? -INFINITY : 8.0f))) {
       // across the four lane groups (rows of 16 lanes) that hold the column
       float a, b;
       swap16(tmax, a, b);
       tmax = fmaxf(a, b);
       swap32(tmax, a, b);
       tmax = fmaxf(a, b);
-    }
-    // The reference maximum moves only when some column's maximum exceeds it by
-    // more than 2^8 (base-2 logits): the weights then stay below 256, well inside
-    // fp16, and the running sums are rescaled rarely (alpha = 0 from the initial
-    // -inf, 1 where a column's maximum did not grow).  Key 0 is visible to every
-    // row, so the first tile sets a finite maximum.
-    if (__builtin_amdgcn_ballot_w64(tmax > m_run + 8.0f)) {
-      const float m_new = fmaxf(m_run, tmax);
+      const float m_new = fmaxf(m_run, tmax + off);
       const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
       ol *= alpha;
 #pragma unroll
       for (int c = 0; c < D / 16; ++c) o[c] *= alpha;
-      m_run = m_new;
+      const float rebase = m_new - off;
+#pragma unroll
+      for (int n = 0; n < 4; ++n)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) s[n][i] -= rebase;
+      cinit = floatx4{-m_new, -m_new, -m_new, -m_new};
     }
     half4 pb[4];
 #pragma unroll
     for (int n = 0; n < 4; ++n)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) pb[n][i] = (_Float16)__builtin_amdgcn_exp2f(s[n][i] - m_run);
+      for (int i = 0; i < 4; ++i) pb[n][i] = (_Float16)__builtin_amdgcn_exp2f(s[n][i]);
     // O^T: dims 16 c + 4 grp + i.  One product covers 32 keys: the lane's 8
     // k slots are keys 32 hh + 4 grp + i and 32 hh + 16 + 4 grp + i (i < 4), the
     // same keys in the V^T operand (A) and in the weights (B = pb[2 hh], pb[2 hh + 1])
