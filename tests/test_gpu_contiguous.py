@@ -223,6 +223,40 @@ def test_prefill_matrix_cores(H, KV, D, M, S, causal, outl, t3):
     assert_close(out, ref, what=f"prefill H={H} KV={KV} D={D} M={M} S={S}")
 
 
+# Long causal prefills (up to 32 query blocks): one and two query heads per
+# workgroup, both head dims, outliers and Student-t K/V, and S > M with a partial
+# last block; a second call gives the same bits.
+@pytest.mark.parametrize("H,KV,D,M,S,outl,t3", [
+    (4, 2, 128, 2048, 2048, False, False),
+    (8, 2, 64, 2048, 2048, True, False),
+    (24, 2, 128, 1536, 1536, False, True),
+    (32, 4, 64, 1536, 1536, False, False),
+    (8, 4, 64, 1000, 1300, False, False)])
+def test_prefill_matrix_cores_long(H, KV, D, M, S, outl, t3):
+    q, t = _pf_inputs(H * 7 + M, H, KV, M, S, D, outl, t3)
+    out = _prefill(q, t, causal=True, num_kv_heads=KV)
+    ref = oa.prefill_per_channel(q.numpy(), *[x.numpy() for x in t], causal=True)
+    assert_close(out, ref, what=f"long prefill H={H} KV={KV} D={D} M={M} S={S}")
+    assert np.array_equal(out, _prefill(q, t, causal=True, num_kv_heads=KV))
+
+
+def test_prefill_matrix_cores_unaligned_rulers():
+    """V scale / zero point views that start 2 bytes into their storage (the
+    epilogue's 8-byte ruler loads then take the 2-byte path)."""
+    q, t = _pf_inputs(12, 8, 2, 200, 400, 64)
+    qd = q.to(DEV)
+    dev_t = [x.to(DEV) for x in t]
+    for i in (4, 5):                                 # v_scale, v_zero
+        big = torch.empty((t[i].numel() + 1,), dtype=t[i].dtype, device=DEV)
+        big[1:] = dev_t[i].reshape(-1)
+        dev_t[i] = big[1:].view(t[i].shape)
+        assert dev_t[i].data_ptr() % 8 != 0
+    out = _kd().kv_dequant_prefill_attention(qd, *dev_t, causal=True, num_kv_heads=2)
+    torch.cuda.synchronize()
+    ref = oa.prefill_per_channel(q.numpy(), *[x.numpy() for x in t], causal=True)
+    assert_close(out.cpu().numpy(), ref, what="unaligned V rulers")
+
+
 def test_prefill_matrix_cores_raw_nibbles_and_tensor_heads():
     """use_quant=False (raw codes), and num_kv_heads < k_packed.shape[0]."""
     q, t = _pf_inputs(9, 8, 4, 100, 300, 64)
