@@ -114,16 +114,25 @@ __global__ void __launch_bounds__(256 * HP) __attribute__((amdgpu_waves_per_eu(D
   const float sc = 1.4426950408889634f * __builtin_amdgcn_rsqf((float)D);
   half8 qh[D / 32], ql[D / 32];
   {
+    // The rulers are read whether or not use_quant is set (the pointers are
+    // always valid), so that every load of the prologue is issued before the
+    // first wait; under a per-element branch each load waited for the previous.
     const uint16_t* qrow = p.q + ((int64_t)h * p.M + mq) * D;
+    uint4 raw[D / 32];
+    uint16_t ksr[D / 32][8];
 #pragma unroll
     for (int j = 0; j < D / 32; ++j) {
-      const uint4 raw = *reinterpret_cast<const uint4*>(qrow + 32 * j + 8 * grp);
-      const uint32_t wds[4] = {raw.x, raw.y, raw.z, raw.w};
+      raw[j] = *reinterpret_cast<const uint4*>(qrow + 32 * j + 8 * grp);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ksr[j][e] = p.ks[(int64_t)kv * D + 32 * j + 8 * grp + e];
+    }
+#pragma unroll
+    for (int j = 0; j < D / 32; ++j) {
+      const uint32_t wds[4] = {raw[j].x, raw[j].y, raw[j].z, raw[j].w};
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const int d = 32 * j + 8 * grp + e;
         float x = hf((uint16_t)(wds[e >> 1] >> (16 * (e & 1)))) * sc;
-        if (quant) x *= hf(p.ks[(int64_t)kv * D + d]);
+        x *= quant ? hf(ksr[j][e]) : 1.0f;
         const _Float16 hi = (_Float16)x;
         qh[j][e] = hi;
         ql[j][e] = (_Float16)(x - (float)hi);
@@ -146,17 +155,25 @@ __global__ void __launch_bounds__(256 * HP) __attribute__((amdgpu_waves_per_eu(D
   // 16 vb + vk + const) hit distinct banks.
   const int vwv = (tid >> 6) & 3;
   const int vk = (lane & 15) + 16 * (vwv & 1), vb = 4 * (vwv >> 1) + (lane >> 4);
-  auto zround = [&](int d) { return quant ? fminf(fmaxf(__builtin_rintf(hf(p.vz[(int64_t)kv * D + d])), 0.f), 15.f) : 0.f; };
+  // zero points rounded and clamped to 0..15 (all loads first, as above)
+  auto zround = [&](uint16_t z) { return quant ? fminf(fmaxf(__builtin_rintf(hf(z)), 0.f), 15.f) : 0.f; };
   // (1024 + zero) of dims 2b and 2b + 1 of the thread's 8, one register per pair;
   // the packed subtractions below take one half of it for both lanes (op_sel)
   half2v vzc[GG::VW][4];
+  {
+    uint16_t zr[GG::VW][8];
 #pragma unroll
-  for (int r = 0; r < GG::VW; ++r)
+    for (int r = 0; r < GG::VW; ++r)
 #pragma unroll
-    for (int b = 0; b < 4; ++b) {
-      vzc[r][b][0] = (_Float16)(1024.0f + zround(8 * (vb + 8 * r) + 2 * b));
-      vzc[r][b][1] = (_Float16)(1024.0f + zround(8 * (vb + 8 * r) + 2 * b + 1));
-    }
+      for (int i = 0; i < 8; ++i) zr[r][i] = p.vz[(int64_t)kv * D + 8 * (vb + 8 * r) + i];
+#pragma unroll
+    for (int r = 0; r < GG::VW; ++r)
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        vzc[r][b][0] = (_Float16)(1024.0f + zround(zr[r][2 * b]));
+        vzc[r][b][1] = (_Float16)(1024.0f + zround(zr[r][2 * b + 1]));
+      }
+  }
   const uint8_t* kbase = p.kp + (int64_t)kv * p.S * (D / 2);
   const uint8_t* vbase = p.vp + (int64_t)kv * p.S * (D / 2);
   // Two register slots of codes: tile k is loaded into slot k % 2 two tiles
