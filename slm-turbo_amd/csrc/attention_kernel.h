@@ -351,11 +351,13 @@ __device__ bool schedule_range(const AttnParams& p, int* misc, int h0, int h1, T
   if (r.T == 0) return false;
   r.lo = range_start(wg, r.T, r.Weff);
   r.hi = range_start(wg + 1, r.T, r.Weff);
-  // locate the sequence holding tile lo
+  // locate the sequence holding tile lo (lengths from the stash where it holds
+  // them: this thread wrote them above, and a global re-read would add a
+  // dependent round trip to every workgroup's start)
   if (r.lo >= my_excl && r.lo < my_excl + mysum) {
     int run = my_excl;
     for (int b = cb0; b < cb1; ++b) {
-      const int t = tiles_of<TT>(seq_len_lane(p, b));
+      const int t = tiles_of<TT>(b < stash_n ? stash[b] : seq_len_lane(p, b));
       if (r.lo < run + t) {
         misc[20] = b;
         misc[21] = run;
