@@ -174,37 +174,41 @@ __global__ void __launch_bounds__(256 * HP) __attribute__((amdgpu_waves_per_eu(D
         vzc[r][b][1] = (_Float16)(1024.0f + zround(zr[r][2 * b + 1]));
       }
   }
-  const uint8_t* kbase = p.kp + (int64_t)kv * p.S * (D / 2);
-  const uint8_t* vbase = p.vp + (int64_t)kv * p.S * (D / 2);
+  // The KV head's code planes from scalar registers, the lane's place in them as
+  // 32-bit offsets (a plane is S * D / 2 < 2^32 bytes): scalar base plus vector
+  // offset loads, and no 64-bit per-lane pointers held across the loop.
+  const int kvs = __builtin_amdgcn_readfirstlane(kv);
+  const uint8_t* const kbase = p.kp + (int64_t)kvs * p.S * (D / 2);
+  const uint8_t* const vbase = p.vp + (int64_t)kvs * p.S * (D / 2);
   // Two register slots of codes: tile k is loaded into slot k % 2 two tiles
   // before it is computed, and written to LDS one tile before.
   uint2 kx[2][GG::KW];
   uint32_t vx[2][GG::VW][2];
-  const uint8_t* const ksrc0 = kbase + (int64_t)kk * (D / 2) + ku * (D / 8);
-  const uint8_t* const vsrc0 = vbase + (int64_t)(2 * vk) * (D / 2) + 4 * vb;
+  const uint32_t koff0 = (uint32_t)(kk * (D / 2) + ku * (D / 8));
+  const uint32_t voff0 = (uint32_t)(2 * vk * (D / 2) + 4 * vb);
   auto load = [&](int t, auto slot) {   // the tile's codes (keys past S re-read key S - 1)
     constexpr int sl = decltype(slot)::value;
     if (!stager) return;
     if ((t + 1) * BN <= p.S) {             // uniform: every key of the tile lies before S
-      const int64_t off = (int64_t)t * BN * (D / 2);
+      const uint32_t off = (uint32_t)t * BN * (D / 2);
 #pragma unroll
-      for (int i = 0; i < GG::KW; ++i) kx[sl][i] = *reinterpret_cast<const uint2*>(ksrc0 + off + 8 * i);
+      for (int i = 0; i < GG::KW; ++i) kx[sl][i] = *reinterpret_cast<const uint2*>(kbase + (koff0 + off + 8 * i));
 #pragma unroll
       for (int r = 0; r < GG::VW; ++r) {
-        vx[sl][r][0] = *reinterpret_cast<const uint32_t*>(vsrc0 + off + 32 * r);
-        vx[sl][r][1] = *reinterpret_cast<const uint32_t*>(vsrc0 + off + D / 2 + 32 * r);
+        vx[sl][r][0] = *reinterpret_cast<const uint32_t*>(vbase + (voff0 + off + 32 * r));
+        vx[sl][r][1] = *reinterpret_cast<const uint32_t*>(vbase + (voff0 + off + D / 2 + 32 * r));
       }
       return;
     }
     const int key = min(t * BN + kk, p.S - 1);
-    const uint8_t* ksrc = kbase + (int64_t)key * (D / 2) + ku * (D / 8);
+    const uint32_t ko = (uint32_t)(key * (D / 2) + ku * (D / 8));
 #pragma unroll
-    for (int i = 0; i < GG::KW; ++i) kx[sl][i] = *reinterpret_cast<const uint2*>(ksrc + 8 * i);
+    for (int i = 0; i < GG::KW; ++i) kx[sl][i] = *reinterpret_cast<const uint2*>(kbase + (ko + 8 * i));
     const int k0 = min(t * BN + 2 * vk, p.S - 1), k1 = min(t * BN + 2 * vk + 1, p.S - 1);
 #pragma unroll
     for (int r = 0; r < GG::VW; ++r) {
-      vx[sl][r][0] = *reinterpret_cast<const uint32_t*>(vbase + (int64_t)k0 * (D / 2) + 4 * (vb + 8 * r));
-      vx[sl][r][1] = *reinterpret_cast<const uint32_t*>(vbase + (int64_t)k1 * (D / 2) + 4 * (vb + 8 * r));
+      vx[sl][r][0] = *reinterpret_cast<const uint32_t*>(vbase + (uint32_t)(k0 * (D / 2) + 4 * (vb + 8 * r)));
+      vx[sl][r][1] = *reinterpret_cast<const uint32_t*>(vbase + (uint32_t)(k1 * (D / 2) + 4 * (vb + 8 * r)));
     }
   };
   auto store = [&](auto slot) {  // slot's codes -> fp16 (code - zero) in LDS stage `slot`
@@ -264,17 +268,24 @@ __global__ void __launch_bounds__(256 * HP) __attribute__((amdgpu_waves_per_eu(D
 
   using S0 = std::integral_constant<int, 0>;
   using S1 = std::integral_constant<int, 1>;
+  // The staging waves' tile loads are issued unconditionally (the last tile
+  // again where no tile t + 2 is left), and the loop below is instantiated
+  // separately for staging and other waves: the compiler's memory-counter waits
+  // are merged conservatively over paths that issue no loads, and with either
+  // branch the staging store of tile t + 1 waited for the loads of tile t + 2
+  // as well, which were issued in the same iteration.
   if (ntiles > 0) {
     load(0, S0{});
-    if (ntiles > 1) load(1, S1{});
+    load(min(1, ntiles - 1), S1{});
     store(S0{});
   }
   __syncthreads();
   // iteration t: tile t is in LDS stage t % 2, tile t + 1 in register slot (t + 1) % 2
-  auto iteration = [&](int t, auto slot) {
+  auto iteration = [&](int t, auto slot, auto role) {
     constexpr int sl = decltype(slot)::value;
+    constexpr bool ST = decltype(role)::value;
     using Next = std::integral_constant<int, sl ^ 1>;
-    if (t + 2 < ntiles) load(t + 2, slot);          // slot sl held tile t, already in LDS
+    if constexpr (ST) load(min(t + 2, ntiles - 1), slot);   // slot sl held tile t, already in LDS
     const uint8_t* Ks = smem + sl * GG::STAGE;
     const uint8_t* Vs = Ks + GG::KBYTES;
     // S^T: keys 16 n + 4 grp + i of this tile against the lane's query
@@ -314,7 +325,9 @@ __global__ void __launch_bounds__(256 * HP) __attribute__((amdgpu_waves_per_eu(D
     // before S and at or before the wave's first row (m0 + 16 w) needs no mask:
     // the test is uniform over the wave.
     const int kt0 = t * BN;
-    const bool whole = kt0 + BN <= p.S && (!p.causal || kt0 + BN - 1 <= m0 + 16 * w);
+    // the wave's first row as a scalar (no vector register held across the loop)
+    const int wrow0 = m0 + __builtin_amdgcn_readfirstlane(16 * w);
+    const bool whole = kt0 + BN <= p.S && (!p.causal || kt0 + BN - 1 <= wrow0);
     float tmax = -INFINITY;
     if (whole) {
 #pragma unroll
@@ -382,13 +395,19 @@ __global__ void __launch_bounds__(256 * HP) __attribute__((amdgpu_waves_per_eu(D
       const half8 b = __builtin_shufflevector(pb[2 * hh], pb[2 * hh + 1], 0, 1, 2, 3, 4, 5, 6, 7);
       ol = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, b, ol, 0, 0, 0);
     }
-    if (t + 1 < ntiles) store(Next{});
+    if constexpr (ST) {
+      if (t + 1 < ntiles) store(Next{});
+    }
     __syncthreads();
   };
-  for (int t = 0; t < ntiles; t += 2) {
-    iteration(t, S0{});
-    if (t + 1 < ntiles) iteration(t + 1, S1{});
-  }
+  auto run = [&](auto role) {
+    for (int t = 0; t < ntiles; t += 2) {
+      iteration(t, S0{}, role);
+      if (t + 1 < ntiles) iteration(t + 1, S1{}, role);
+    }
+  };
+  if (stager) run(std::true_type{});
+  else run(std::false_type{});
 
   // every row of the ones product holds the column's whole sum
   const float rl = 1.0f / ol[0];
