@@ -49,9 +49,11 @@ quantize_store_kernel(const uint16_t* __restrict__ key, int64_t key_stride,
   if (row >= N * KV) return;                       // wave-uniform
   const int64_t t = row / KV;
   const int h = (int)(row - t * KV);
+  // The row is quantized whether or not its slot is valid and only the stores
+  // test it: with an early exit on the slot the row's K/V loads were issued
+  // after the slot's had returned, two dependent round trips per call.
   const int64_t slot = slot_mapping[t];
-  if (slot < 0 || slot >= num_slots) return;       // padding token / out of range
-
+  const bool valid = slot >= 0 && slot < num_slots;   // padding token / out of range: no store
   const bool active = lane < HALF;
   const int li = active ? lane : 0;
   const uint32_t kw = *reinterpret_cast<const uint32_t*>(key + t * key_stride + (int64_t)h * D + 2 * li);
@@ -67,6 +69,7 @@ quantize_store_kernel(const uint16_t* __restrict__ key, int64_t key_stride,
   quantize_pair<D>(k0, k1, kmin, kstep, kb);
   quantize_pair<D>(v0, v1, vmin, vstep, vb);
 
+  if (!valid) return;
   uint8_t* dst = cache + (slot * KV + h) * (int64_t)SLOT;
   if (active) {
     dst[lane] = kb;
