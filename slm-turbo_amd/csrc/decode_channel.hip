@@ -84,7 +84,10 @@ __global__ void __launch_bounds__(64 * NW) split_kernel(const Params p) {
   const int h0 = kv * p.G;
 
   // round r's codes: lane (key t, quarter c) loads its quarter of key t's K and
-  // V rows (zeros past the wave's keys); round 0's loads fly while q' is prepared
+  // V rows; round 0's loads fly while q' is prepared.  Keys past the wave's
+  // re-read the chunk's last key (their scores are never stored and their V
+  // rows never read): selecting zeros instead made each load wait before the
+  // next was issued.
   const int t = lane >> 2, c = lane & 3;
   const uint8_t* kbase = p.kp + ((int64_t)kv * p.S + tok0 + wk0) * VB + c * QB;
   const uint8_t* vbase = p.vp + ((int64_t)kv * p.S + tok0 + wk0) * VB + c * QB;
@@ -93,35 +96,50 @@ __global__ void __launch_bounds__(64 * NW) split_kernel(const Params p) {
   };
   auto load_round = [&](int r) -> Codes {
     Codes cd;
-    const int j = 16 * r + t;
+    const int j = min(wk0 + 16 * r + t, ntok - 1) - wk0;   // a key of the chunk
 #pragma unroll
     for (int i = 0; i < QB / 8; ++i) {
-      cd.k[i] = j < wn ? *reinterpret_cast<const uint2*>(kbase + (int64_t)j * VB + 8 * i) : make_uint2(0u, 0u);
-      cd.v[i] = j < wn ? *reinterpret_cast<const uint2*>(vbase + (int64_t)j * VB + 8 * i) : make_uint2(0u, 0u);
+      cd.k[i] = *reinterpret_cast<const uint2*>(kbase + (int64_t)j * VB + 8 * i);
+      cd.v[i] = *reinterpret_cast<const uint2*>(vbase + (int64_t)j * VB + 8 * i);
     }
     return cd;
   };
   Codes cur = load_round(0);
 
-  // q' (straight-line, so every load is in flight at once) and this lane's V
-  // rulers for the output dims 2b, 2b+1
+  // q' and this lane's V rulers for the output dims 2b, 2b+1.  Every load is
+  // issued first, unconditionally (rows past G re-read the last head's, the
+  // rulers are read without use_quant): under per-element branches each load
+  // waited for the one before it.
   const int b = lane % NB, par = lane / NB, step = 64 / NB;
+  constexpr int QN = (GT * D + 64 * NW - 1) / (64 * NW);   // q' elements per thread
+  uint16_t qraw[QN], kraw[QN], vsr[2], vzw[2];
+#pragma unroll
+  for (int u = 0; u < QN; ++u) {
+    const int i = min(tid + u * 64 * NW, GT * D - 1);
+    const int h = min(i / D, p.G - 1), d = i % D;
+    qraw[u] = p.q[(int64_t)(h0 + h) * D + d];
+    kraw[u] = p.ks[(int64_t)kv * D + d];
+  }
+#pragma unroll
+  for (int e = 0; e < 2; ++e) {
+    vsr[e] = p.vs[(int64_t)kv * D + 2 * b + e];
+    vzw[e] = p.vz[(int64_t)kv * D + 2 * b + e];
+  }
   float vsc[2] = {1.f, 1.f}, vzr[2] = {0.f, 0.f};
   if (quant) {
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
-      vsc[e] = h2f(p.vs[(int64_t)kv * D + 2 * b + e]);
-      vzr[e] = h2f(p.vz[(int64_t)kv * D + 2 * b + e]);
+      vsc[e] = h2f(vsr[e]);
+      vzr[e] = h2f(vzw[e]);
     }
   }
-  for (int i = tid; i < GT * D; i += 64 * NW) {
-    const int h = i / D, d = i % D;
-    float x = 0.f;
-    if (h < p.G) {
-      x = h2f(p.q[(int64_t)(h0 + h) * D + d]);
-      if (quant) x *= h2f(p.ks[(int64_t)kv * D + d]);
+#pragma unroll
+  for (int u = 0; u < QN; ++u) {
+    const int i = tid + u * 64 * NW;
+    if (i < GT * D) {
+      const float x = h2f(qraw[u]) * (quant ? h2f(kraw[u]) : 1.f);
+      qs[i] = i / D < p.G ? x : 0.f;
     }
-    qs[i] = x;
   }
   __syncthreads();
 
