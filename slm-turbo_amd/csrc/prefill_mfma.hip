@@ -69,7 +69,13 @@ constexpr int BN = 64;   // keys per tile
 
 template <int D>
 struct Geo {
-  static constexpr int KROW = D * 2 + 16;   // bytes of a staged K row
+  // Bytes of a staged K row: 32 bytes of padding.  The LDS serves a 16-byte read
+  // for lanes 0-7 and 16-23 (then 8-15 and 24-31, ...) together, over 64 banks;
+  // the K operand read puts rows 16 n + 0..7 at word offset 0 and 4 of a row in
+  // one such group, and only a row stride of 8 (mod 16) words keeps those 16
+  // four-bank spans apart.  Rows of 16 bytes of padding (36 or 68 words) cost
+  // 4 conflict cycles per read.
+  static constexpr int KROW = D * 2 + 32;
   static constexpr int VROW = BN * 2 + 8;   // bytes of a staged V^T row
   static constexpr int KBYTES = BN * KROW;
   static constexpr int STAGE = KBYTES + D * VROW;
@@ -143,9 +149,8 @@ __global__ void __launch_bounds__(256 * HP) __attribute__((amdgpu_waves_per_eu(D
   // ---- staging roles
   // K: thread (key kk, quarter ku): dims D/4 * ku .. + D/4 - 1.  Staging wave v
   // takes keys 16 v .. 16 v + 15, lane l key 16 v + (l & 15) and quarter l >> 4:
-  // the lanes of a quarter write consecutive rows of a 36- (68-) word stride,
-  // which start 4 banks apart, and the wave's loads cover its 16 keys' codes
-  // contiguously.
+  // the lanes of a quarter write consecutive rows, and the wave's loads cover
+  // its 16 keys' codes contiguously.
   const int kk = (tid & 15) + 16 * ((tid >> 6) & 3), ku = (tid >> 4) & 3;
   const half2v kzc = half2v{(_Float16)1024.0f, (_Float16)1024.0f};
   // V: thread (key pair vk, byte group vb (+ 8)): dims 8 vb .. 8 vb + 7, each with
