@@ -76,7 +76,11 @@ struct Geo {
   // four-bank spans apart.  Rows of 16 bytes of padding (36 or 68 words) cost
   // 4 conflict cycles per read.
   static constexpr int KROW = D * 2 + 32;
-  static constexpr int VROW = BN * 2 + 8;   // bytes of a staged V^T row
+  // Bytes of a staged V^T row (keys in the order vpos gives, 32 bytes of
+  // padding): the P.V operand of a lane is 16 contiguous bytes, one 16-byte read
+  // (an 8-byte pair read moves half the bytes per cycle), conflict-free at a
+  // stride of 40 words like the K rows.
+  static constexpr int VROW = BN * 2 + 32;
   static constexpr int KBYTES = BN * KROW;
   static constexpr int STAGE = KBYTES + D * VROW;
   static constexpr int LDS = 2 * STAGE;
@@ -85,6 +89,12 @@ struct Geo {
 };
 
 __device__ __forceinline__ float hf(uint16_t h) { return h2f(h); }
+
+// Position of key k (of a 64-key tile) in a V^T row: key 32 h + 16 u + 4 g + i
+// (i < 4) sits at 32 h + 8 g + 4 u + i, so that the 8 keys of lane group g in
+// the P.V product of half h (keys 32 h + 4 g + i, then 32 h + 16 + 4 g + i)
+// are contiguous.  Even keys stay even: a key pair stays one 4-byte word.
+__device__ __forceinline__ int vpos(int k) { return (k & 32) | ((k & 12) << 1) | ((k & 16) >> 2) | (k & 3); }
 
 // fp16 pairs (1024 + low nibble, 1024 + high nibble) of byte i of x, minus zc
 __device__ __forceinline__ uint32_t nib_pair(uint32_t lo_all, uint32_t hi_all, int i, half2v zc) {
@@ -154,12 +164,12 @@ __global__ void __launch_bounds__(256 * HP) __attribute__((amdgpu_waves_per_eu(D
   const int kk = (tid & 15) + 16 * ((tid >> 6) & 3), ku = (tid >> 4) & 3;
   const half2v kzc = half2v{(_Float16)1024.0f, (_Float16)1024.0f};
   // V: thread (key pair vk, byte group vb (+ 8)): dims 8 vb .. 8 vb + 7, each with
-  // 1024 + its rounded zero point.  A staging wave takes 16 key pairs x 4 byte
-  // groups, lane l key pair (l & 15) and byte group l >> 4, so that the lanes of
-  // one V^T store (row d = 8 vb + const, word vk of a 34-word row: bank
-  // 16 vb + vk + const) hit distinct banks.
-  const int vwv = (tid >> 6) & 3;
-  const int vk = (lane & 15) + 16 * (vwv & 1), vb = 4 * (vwv >> 1) + (lane >> 4);
+  // 1024 + its rounded zero point.  Staging wave v takes all 32 key pairs of the
+  // tile for byte groups 2 v and 2 v + 1 (lane l: key pair l & 31, byte group
+  // 2 v + (l >> 5)); its V^T stores then cover two rows' 32 words each, which
+  // the LDS writes without bank conflicts.
+  const int vk = lane & 31, vb = 2 * ((tid >> 6) & 3) + (lane >> 5);
+  const int vcol = 2 * vpos(2 * vk);   // byte offset of the pair in a V^T row
   // zero points rounded and clamped to 0..15 (all loads first, as above)
   auto zround = [&](uint16_t z) { return quant ? fminf(fmaxf(__builtin_rintf(hf(z)), 0.f), 15.f) : 0.f; };
   // (1024 + zero) of dims 2b and 2b + 1 of the thread's 8, one register per pair;
@@ -250,8 +260,8 @@ __global__ void __launch_bounds__(256 * HP) __attribute__((amdgpu_waves_per_eu(D
         const half2v zo = __builtin_shufflevector(vzc[r][b], vzc[r][b], 1, 1);
         const half2v e = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(lo1, lo0, sel) | 0x64006400u) - ze;
         const half2v o = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(hi1, hi0, sel) | 0x64006400u) - zo;
-        *reinterpret_cast<uint32_t*>(Vs + d * GG::VROW + 4 * vk) = __builtin_bit_cast(uint32_t, e);
-        *reinterpret_cast<uint32_t*>(Vs + (d + 1) * GG::VROW + 4 * vk) = __builtin_bit_cast(uint32_t, o);
+        *reinterpret_cast<uint32_t*>(Vs + d * GG::VROW + vcol) = __builtin_bit_cast(uint32_t, e);
+        *reinterpret_cast<uint32_t*>(Vs + (d + 1) * GG::VROW + vcol) = __builtin_bit_cast(uint32_t, o);
       }
     }
   };
@@ -315,17 +325,13 @@ __global__ void __launch_bounds__(256 * HP) __attribute__((amdgpu_waves_per_eu(D
     }
     // The V^T operands of the tile, read now so that their LDS latency hides
     // behind the softmax: dims 16 c + col, keys 32 hh + 4 grp + i and
-    // 32 hh + 16 + 4 grp + i (i < 4).
+    // 32 hh + 16 + 4 grp + i (i < 4), positions 32 hh + 8 grp .. + 7 of the row.
     half8 va[D / 16][2];
 #pragma unroll
     for (int c = 0; c < D / 16; ++c)
 #pragma unroll
-      for (int hh = 0; hh < 2; ++hh) {
-        const uint8_t* vrow = Vs + (16 * c + col) * GG::VROW;
-        const half4 a0 = *reinterpret_cast<const half4*>(vrow + (32 * hh + 4 * grp) * 2);
-        const half4 a1 = *reinterpret_cast<const half4*>(vrow + (32 * hh + 16 + 4 * grp) * 2);
-        va[c][hh] = __builtin_shufflevector(a0, a1, 0, 1, 2, 3, 4, 5, 6, 7);
-      }
+      for (int hh = 0; hh < 2; ++hh)
+        va[c][hh] = *reinterpret_cast<const half8*>(Vs + (16 * c + col) * GG::VROW + (32 * hh + 8 * grp) * 2);
     // Keys past S or past a causal row are masked.  A tile whose keys all lie
     // before S and at or before the wave's first row (m0 + 16 w) needs no mask:
     // the test is uniform over the wave.
