@@ -65,6 +65,7 @@ using namespace attn;
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) const uint64_t lds_u64;
 
 template <int D, int NKV, int WPK>
 struct Shape {
@@ -288,7 +289,7 @@ __global__ void __launch_bounds__(NKV * WPK * 64) mfma_kernel(const AttnParams p
   const int col = lane & 15, grp = lane >> 4;
   const int hq = col >> 2, lx = col & 3;
   // first of the 16 dims that k-block kb of lane group grp covers (QK)
-  auto kbase = [&](int kb) { return D == 128 ? 32 * grp + 16 * kb : 16 * grp; };
+  auto kbase = [&](int kb) { return 64 * kb + 16 * grp; };
   const uint8_t* const qsl = smem + S::QOFF + wave * 1024;
 
   v4i qb[NSET][KB];                    // A operand: limb lx of head set st's head hq, k-set grp
@@ -389,9 +390,12 @@ __global__ void __launch_bounds__(NKV * WPK * 64) mfma_kernel(const AttnParams p
   // ---------------------------------------------------------------- tile data
   // LDS reads of one tile for this lane: QK A rows (packed), the rulers of the
   // lane's softmax tokens, and the V byte pairs of its PV k-slots.
-  // K: lane (row col, group grp) reads bytes [16 grp, 16 grp + 16) of its row's
-  // codes (head_dim 64: [8 grp, 8 grp + 8)); 8 consecutive rows of an odd-unit
-  // stride start in 8 different 4-bank groups.
+  // K: lane (row col, group grp) reads bytes [8 grp, 8 grp + 8) of each 32-byte
+  // half (k-block) of its row's codes, so that k-block kb is dims 64 kb ..
+  // 64 kb + 63 in order.  These 8-byte reads are free of LDS bank conflicts at
+  // the staged row strides; 8-byte reads 16 bytes apart, and pair reads
+  // (ds_read2_b64) of 8-byte halves 8 or 32 bytes apart, cost 2, 8 and 8
+  // conflict cycles each.
   // V: lane (row col, group grp) reads bytes [4 col, 4 col + 4) (head_dim 64:
   // [2 col, 2 col + 2)) of the V codes of its 8 k-slot tokens.
   // With the token split, the wave reads only its half of the tile's tokens
@@ -406,19 +410,15 @@ __global__ void __launch_bounds__(NKV * WPK * 64) mfma_kernel(const AttnParams p
 #pragma unroll
     for (int rb = 0; rb < RBW; ++rb) {
       const uint8_t* row = Sb + (16 * rb + col) * S::RSTRIDE;
-      if constexpr (D == 128) {
-        // a sub-row starts 8-byte aligned (136-byte slots): two 8-byte halves
-        // (one ds_read2_b64)
-        const uint2 w0 = *reinterpret_cast<const uint2*>(row + 16 * grp);
-        const uint2 w1 = *reinterpret_cast<const uint2*>(row + 16 * grp + 8);
-        R.k[rb][0] = w0.x;
-        R.k[rb][1] = w0.y;
-        R.k[rb][2] = w1.x;
-        R.k[rb][3] = w1.y;
-      } else {
-        const uint2 w = *reinterpret_cast<const uint2*>(row + 8 * grp);
-        R.k[rb][0] = w.x;
-        R.k[rb][1] = w.y;
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) {
+        // the second k-block's address passes through an empty asm, which keeps
+        // the compiler from merging the two reads into one pair read
+        const lds_u64* src = (const lds_u64*)(row + 32 * kb + 8 * grp);
+        if (kb > 0) asm("" : "+v"(src));
+        const uint64_t w = *src;
+        R.k[rb][2 * kb] = (uint32_t)w;
+        R.k[rb][2 * kb + 1] = (uint32_t)(w >> 32);
       }
     }
 #pragma unroll
