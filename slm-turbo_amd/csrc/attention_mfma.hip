@@ -478,11 +478,12 @@ __global__ void __launch_bounds__(NKV * WPK * 64) mfma_kernel(const AttnParams p
     v += dpp_f<DPP_QUAD_XOR2>(v);
     return v + dpp_f<DPP_QUAD_XOR1>(v);
   };
-  // value of head `col` (0..3) for the PV lanes: from lane 16 col, which holds head col
+  // value of head `col` (0..3) for the PV lanes: from lane 16 (col & 3), which
+  // holds head col & 3 (one cross-lane read; four lane reads and a per-lane
+  // choice among them compiled to a branch chain)
+  const int pv_src = 64 * (col & 3);
   auto for_pv_lane = [&](float v) {
-    const float v0 = readlane_f(v, 0), v1 = readlane_f(v, 16), v2 = readlane_f(v, 32), v3 = readlane_f(v, 48);
-    const int c = col & 3;
-    return c == 0 ? v0 : c == 1 ? v1 : c == 2 ? v2 : v3;
+    return __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(pv_src, __builtin_bit_cast(int, v)));
   };
   // value of head `col` (0..HPW-1) for the PV lanes: head col & 3 of set col >> 2
   auto for_pv_lane_set = [&](const float (&v)[NSET]) {
