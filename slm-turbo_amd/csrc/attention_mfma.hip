@@ -304,9 +304,9 @@ __global__ void __launch_bounds__(NKV * WPK * 64) mfma_kernel(const AttnParams p
 
   // Value of head grp for the softmax lanes, from lane 4 grp (which holds head
   // grp in the query operand's layout).
+  const int soft_src = 16 * grp;   // byte address of lane 4 grp
   auto for_soft_lane = [&](float v) {
-    const float v0 = readlane_f(v, 0), v1 = readlane_f(v, 4), v2 = readlane_f(v, 8), v3 = readlane_f(v, 12);
-    return grp == 0 ? v0 : grp == 1 ? v1 : grp == 2 ? v2 : v3;
+    return __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(soft_src, __builtin_bit_cast(int, v)));
   };
   // Query of head set st for a new segment: read the lane's 16 dims per k-block
   // straight from the query slot (with the token split, set st's heads are in
