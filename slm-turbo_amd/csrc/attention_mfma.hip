@@ -114,6 +114,14 @@ struct Shape {
   static_assert(LDS <= 160 * 1024, "LDS ring too large");
 };
 
+// The weights' reference sits kRefMargin (base 2) above the largest score seen:
+// weights stay below 2^-kRefMargin (so p * step never exceeds the fp16 step), and
+// the reference moves, with its rescale of the sums, only when a score passes it.
+// Placed at the maximum itself it moved in most tiles of a short range (any of a
+// wave's 4 or 8 heads growing): 21.4 -> 21.0 us per step at 32 q / 4 KV heads,
+// head_dim 64, batch 32, 4096 keys.
+constexpr float kRefMargin = 4.0f;
+
 // log2(e) / sqrt(D)
 template <int D>
 constexpr float kC = D == 128 ? 1.4426950408889634f / 11.313708498984761f : 1.4426950408889634f / 8.0f;
@@ -293,7 +301,8 @@ __global__ void __launch_bounds__(NKV * WPK * 64) mfma_kernel(const AttnParams p
   const uint8_t* const qsl = smem + S::QOFF + wave * 1024;
 
   v4i qb[NSET][KB];                    // A operand: limb lx of head set st's head hq, k-set grp
-  float qa[NSET], qs[NSET], mq[NSET], m_run[NSET], l_run[NSET], vmt[NSET];
+  // m_run: the weights' reference, in score units (see softmax); dq: its margin
+  float qa[NSET], qs[NSET], mq[NSET], m_run[NSET], l_run[NSET], vmt[NSET], dq[NSET];
 #pragma unroll
   for (int st = 0; st < NSET; ++st) {
     qa[st] = qs[st] = mq[st] = 0.f;
@@ -377,6 +386,7 @@ __global__ void __launch_bounds__(NKV * WPK * 64) mfma_kernel(const AttnParams p
     }
     qs[st] = for_soft_lane(qsum);
     qa[st] = for_soft_lane(__builtin_amdgcn_ldexpf(kC<D>, -sc));
+    dq[st] = kRefMargin * __builtin_amdgcn_rcpf(qa[st]);
   };
   auto begin = [&]() __attribute__((always_inline)) {
 #pragma unroll
@@ -532,10 +542,11 @@ __global__ void __launch_bounds__(NKV * WPK * 64) mfma_kernel(const AttnParams p
       if (__builtin_amdgcn_ballot_w64(tl > m_run[st])) {
         const float tmax = head_max(tl);
         const bool grow = tmax > m_run[st];
-        alpha[st] = grow ? __builtin_amdgcn_exp2f((m_run[st] - tmax) * qa[st]) : 1.f;   // 0 from -inf
+        const float mnew = tmax + dq[st];
+        alpha[st] = grow ? __builtin_amdgcn_exp2f((m_run[st] - mnew) * qa[st]) : 1.f;   // 0 from -inf
         l_run[st] *= alpha[st];
         vmt[st] *= alpha[st];
-        m_run[st] = grow ? tmax : m_run[st];
+        m_run[st] = grow ? mnew : m_run[st];
         mq[st] = m_run[st] * qa[st];
         grew = true;
       }
