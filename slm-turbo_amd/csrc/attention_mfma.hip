@@ -34,16 +34,17 @@
 //
 // PV: v_mfma_f32_16x16x32_f16 with A = V^T (rows: 16 V bytes, one of their two
 // nibbles; k: 32 tokens) and B = the fp16 weights (columns: the wave's 4 heads).
-// A V byte pair of one token is read with ds_read_u16, two tokens are packed
-// with one v_perm, and each nibble becomes an fp16 subnormal n * 2^-24 (or
-// 16 n * 2^-24) with one AND, which the matrix core multiplies exactly by the
-// weight.  Weights w = fp16(p * step) go into the B columns of the wave's
-// heads; the columns the heads leave free carry each weight's remainder,
-// fp16((p * step - w) * 2^11), so a column pair holds p * step to ~22 bits
-// down to 2^-25 and to within 2^-36 below (a lone fp16 weight loses precision
-// below 2^-14 and vanishes below 2^-25: a long tail behind a dominant token
-// would drop out).  The pair is joined once per segment; the softmax sums use
-// p itself, and the per-token min enters once per token as sum(p * min).
+// A lane's V bytes of one token are one ds_read_u16 (head_dim 64) or ds_read_b32
+// (128), two tokens are packed with one v_perm, and each nibble becomes an fp16
+// subnormal n * 2^-24 (or 16 n * 2^-24) with one AND, which the matrix core
+// multiplies exactly by the weight.  Weights w = fp16(p * step) go into the B
+// columns of the wave's heads; the columns the heads leave free carry each
+// weight's remainder, fp16((p * step - w) * 2^11), so a column pair holds
+// p * step to ~22 bits down to 2^-25 and to within 2^-36 below (a lone fp16
+// weight loses precision below 2^-14 and vanishes below 2^-25: a long tail
+// behind a dominant token would drop out).  The pair is joined once per
+// segment; the softmax sums use p itself, and the per-token min enters once per
+// token as sum(p * min).
 #include "attention_kernel.h"
 
 #include <hip/hip_ext.h>

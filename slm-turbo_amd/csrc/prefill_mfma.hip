@@ -5,8 +5,8 @@
 // Prefill is GEMM-shaped (every key meets up to 64 query rows of a tile), so
 // unlike the decode it runs on the matrix cores.  A workgroup takes 64 query rows
 // of one query head (of two, for long prefills), one wave per 16 rows of a head,
-// and walks the 64-key tiles the rows can see.  Everything is kept transposed, so a lane owns one query column from
-// the scores to the output:
+// and walks the 64-key tiles the rows can see.  Everything is kept transposed,
+// so a lane owns one query column from the scores to the output:
 //   S^T = K Q'^T     (v_mfma_f32_16x16x32_f16: A = K rows, B = the lane's query)
 //   P^T = exp2(S^T - m)      (online softmax per query column)
 //   O^T += V^T P^T   (v_mfma_f32_16x16x32_f16: B = the lane's P^T blocks as they are)
@@ -34,9 +34,9 @@
 // heads of the same KV head (8 waves) for long prefills; the first four waves
 // stage the tiles for all of them.
 // Staging: the workgroup converts each tile into a 2-stage LDS ring: K as
-// [key][dim] fp16 rows padded to D*2+16 bytes (16-byte operand reads of 8 rows at
-// once hit 8 disjoint bank groups), V^T as [dim][key] fp16 rows padded to 136
-// bytes (8-byte reads of 16 rows hit 16 disjoint bank pairs).  The next tile's
+// [key][dim] fp16 rows of D*2+32 bytes, V^T as [dim][key] fp16 rows of 160 bytes
+// with the keys in the order the P.V product takes them, so that every operand
+// read, K and V^T, is one conflict-free 16-byte read (see Geo).  The next tile's
 // codes are loaded into registers two tiles ahead and written to LDS after the
 // current tile's products; one barrier per tile.  Within a tile, all K operand
 // reads are issued before the first QK product and all V^T operand reads
