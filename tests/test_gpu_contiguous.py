@@ -240,6 +240,26 @@ def test_prefill_matrix_cores_long(H, KV, D, M, S, outl, t3):
     assert np.array_equal(out, _prefill(q, t, causal=True, num_kv_heads=KV))
 
 
+# The two 4096-query causal prefills that bench.py --op-level times (two query
+# heads per workgroup, every query block from 1 to 64 key tiles): heads spread
+# over every KV head checked against the oracle head by head, and a second call
+# gives the same bits.
+@pytest.mark.parametrize("H,KV,D,heads", [
+    (32, 4, 64, (0, 9, 18, 31)),
+    (12, 2, 128, (0, 5, 6, 11))])
+def test_prefill_matrix_cores_bench_shapes(H, KV, D, heads):
+    S = 4096
+    q, t = _pf_inputs(H + D, H, KV, S, S, D)
+    out = _prefill(q, t, causal=True, num_kv_heads=KV)
+    G = H // KV
+    for h in heads:
+        kv = h // G
+        kvt = [x[kv:kv + 1].numpy() for x in t]
+        ref = oa.prefill_per_channel(q[h:h + 1].numpy(), *kvt, causal=True)
+        assert_close(out[h:h + 1], ref, what=f"bench-shape prefill H={H} KV={KV} D={D} head {h}")
+    assert np.array_equal(out, _prefill(q, t, causal=True, num_kv_heads=KV))
+
+
 def test_prefill_matrix_cores_unaligned_rulers():
     """V scale / zero point views that start 2 bytes into their storage (the
     epilogue's 8-byte ruler loads then take the 2-byte path)."""
